@@ -1,0 +1,427 @@
+// matvec.hip - batch-1 (and small-batch) quantized matrix-vector products on
+// gfx950: matvec_<kind> / matvec3 / matvec2 / matmul of the reference
+// (crates/aot-kernels/src/matvec.rs:300-583), bit-exact with its avx2+f16c
+// kernels (simd_avx2.rs):
+//   * K-quants: the per-super-block integer sums are exact (v_dot4 on
+//     unpacked nibbles), then the f32 fold `sum += d*sumi - dmin*summ` runs
+//     sequentially over super-blocks in the reference's order.
+//   * Q8_0/Q4_0/Q5_0: the avx2 kernels keep 8 f32 lanes, lane l accumulating
+//     fma(d*y.d, (f32) sum of products 4l..4l+3, acc_l) over blocks, then a
+//     fixed horizontal sum; reproduced with 8 chains per row.
+//   * F16/BF16/F32: 8 fma chains over 8-element groups, the same horizontal
+//     sum, then the scalar tail.
+// Weights are streamed once with 16-byte loads; the input vector is tiny and
+// stays in L2/L1.
+#include "device.hpp"
+#include "internal.hpp"
+
+namespace aotk {
+
+constexpr int MAX_SEG = 3;
+
+struct MvArgs {
+    const uint8_t *w[MAX_SEG];   // plane 0
+    const uint8_t *w1[MAX_SEG];  // plane 1 (f16 scales) or null
+    const uint8_t *w2[MAX_SEG];  // plane 2 (Q5_0 qh) or null
+    float *y[MAX_SEG];
+    const float *add[MAX_SEG];
+    int rows[MAX_SEG];
+    int nseg, total_rows;
+    int nb;        // blocks per row
+    size_t rb;     // bytes per row in plane 0 (row-major kinds)
+    size_t cols;
+    // activation (token t at offset t * cols / nb)
+    const int8_t *xq;
+    const float *xd;
+    const int16_t *xbs;
+    const float *xf;
+};
+
+__device__ __forceinline__ int seg_of(const MvArgs &a, int row, int &local) {
+    int s = 0;
+    local = row;
+    while (s + 1 < a.nseg && local >= a.rows[s]) {
+        local -= a.rows[s];
+        s++;
+    }
+    return s;
+}
+
+__device__ __forceinline__ void store_row(const MvArgs &a, int grow, int tok, float v) {
+    int local;
+    int s = seg_of(a, grow, local);
+    size_t at = (size_t)tok * a.rows[s] + local;
+    float r = a.add[s] ? a.add[s][at] + v : v;
+    a.y[s][at] = r;
+}
+
+// --------------------------------------------------------------- K-quants
+// Wave = R rows. Lane = 8*g + p: super-block slot g (8 per step), part p
+// (32 of the block's 256 values). Integer sums are reduced over the 8 lanes of
+// a slot, then the per-super-block f32 terms are folded in order.
+template <int KIND, int R>
+__global__ __launch_bounds__(256) void k_mv_kquant(MvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int tok = blockIdx.y;
+    const int grow0 = (blockIdx.x * 4 + wave) * R;
+    if (grow0 >= a.total_rows) return;
+    const int g = lane >> 3, p = lane & 7;
+    const int nb = a.nb;
+    const int8_t *xq = a.xq + (size_t)tok * a.cols;
+    const float *xd = a.xd + (size_t)tok * nb;
+    const int16_t *xbs = a.xbs + (size_t)tok * nb * 16;
+
+    const uint8_t *wrow[R];
+    const uint16_t *drow[R];
+    bool rvalid[R];
+    for (int r = 0; r < R; r++) {
+        int grow = grow0 + r;
+        rvalid[r] = grow < a.total_rows;
+        int local;
+        int s = seg_of(a, rvalid[r] ? grow : grow0, local);
+        if (KIND == AOTK_Q6_K) {
+            wrow[r] = a.w[s] + (size_t)local * nb * 208;
+            drow[r] = (const uint16_t *)a.w1[s] + (size_t)local * nb;
+        } else {
+            wrow[r] = a.w[s] + (size_t)local * a.rb;
+            drow[r] = nullptr;
+        }
+    }
+    float acc[R];
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+
+    // lane-constant geometry
+    int y_lo, y_hi, bs_lo, bs_hi;
+    if (KIND == AOTK_Q6_K) {
+        const int n = p >> 2, half = (p >> 1) & 1, which = p & 1;
+        y_lo = 128 * n + 32 * which + 16 * half;
+        y_hi = y_lo + 64;
+        bs_lo = y_lo / 16;
+        bs_hi = y_hi / 16;
+    } else {
+        const int j = p >> 1, h = p & 1;
+        y_lo = 64 * j + 16 * h;
+        y_hi = y_lo + 32;
+        bs_lo = 4 * j + h;
+        bs_hi = bs_lo + 2;
+    }
+
+    for (int sb0 = 0; sb0 < nb; sb0 += 8) {
+        const int sb = sb0 + g;
+        const bool valid = sb < nb;
+        const int sbc = valid ? sb : nb - 1;
+        const uint4 ylo = *(const uint4 *)(xq + (size_t)sbc * 256 + y_lo);
+        const uint4 yhi = *(const uint4 *)(xq + (size_t)sbc * 256 + y_hi);
+        const float yd = xd[sbc];
+        const int bslo = xbs[(size_t)sbc * 16 + bs_lo];
+        const int bshi = xbs[(size_t)sbc * 16 + bs_hi];
+        const uint32_t ylw[4] = {ylo.x, ylo.y, ylo.z, ylo.w};
+        const uint32_t yhw[4] = {yhi.x, yhi.y, yhi.z, yhi.w};
+
+        for (int r = 0; r < R; r++) {
+            int sumi = 0, summ = 0;
+            float dd = 0.0f, dm = 0.0f;
+            if (KIND == AOTK_Q4_K || KIND == AOTK_Q5_K) {
+                constexpr int TS = KIND == AOTK_Q4_K ? 144 : 176;
+                constexpr int QS = KIND == AOTK_Q4_K ? 16 : 48;
+                const uint8_t *b = wrow[r] + (size_t)sbc * TS;
+                const uint4 hdr = *(const uint4 *)b;
+                const uint4 q = *(const uint4 *)(b + QS + 16 * p);
+                const int j = p >> 1, h = p & 1;
+                int sc_lo, m_lo, sc_hi, m_hi;
+                scale_min_k4(2 * j, hdr.y, hdr.z, hdr.w, sc_lo, m_lo);
+                scale_min_k4(2 * j + 1, hdr.y, hdr.z, hdr.w, sc_hi, m_hi);
+                const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+                uint32_t hw[4] = {0, 0, 0, 0};
+                if (KIND == AOTK_Q5_K) {
+                    const uint4 qh = *(const uint4 *)(b + 16 + 16 * h);
+                    hw[0] = qh.x; hw[1] = qh.y; hw[2] = qh.z; hw[3] = qh.w;
+                }
+                int slo = 0, shi = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    uint32_t lo = qw[k] & 0x0F0F0F0Fu;
+                    uint32_t hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
+                    if (KIND == AOTK_Q5_K) {
+                        lo |= ((hw[k] >> (2 * j)) & 0x01010101u) << 4;
+                        hi |= ((hw[k] >> (2 * j + 1)) & 0x01010101u) << 4;
+                    }
+                    slo = dot4(lo, ylw[k], slo);
+                    shi = dot4(hi, yhw[k], shi);
+                }
+                sumi = sc_lo * slo + sc_hi * shi;
+                summ = m_lo * bslo + m_hi * bshi;
+                dd = f16_to_f32(hdr.x & 0xFFFFu) * yd;
+                dm = f16_to_f32(hdr.x >> 16) * yd;
+            } else {  // Q6_K
+                const int n = p >> 2, half = (p >> 1) & 1, which = p & 1;
+                const uint8_t *b = wrow[r] + (size_t)sbc * 208;
+                const uint4 ql = *(const uint4 *)(b + 64 * n + 32 * which + 16 * half);
+                const uint4 qh = *(const uint4 *)(b + 128 + 32 * n + 16 * half);
+                const uint32_t scw = *(const uint32_t *)(b + 192 + 8 * n);  // sc[8n .. 8n+3]
+                const uint32_t scw2 = *(const uint32_t *)(b + 192 + 8 * n + 4);
+                const int is_lo = half + 2 * which, is_hi = is_lo + 4;  // index within sc[8n..8n+8]
+                auto sc_at = [&](int i) -> int {
+                    uint32_t w = i < 4 ? scw : scw2;
+                    return (int)(int8_t)((w >> (8 * (i & 3))) & 0xFFu);
+                };
+                const int sh_lo = 2 * which, sh_hi = 4 + 2 * which;
+                const uint32_t lw[4] = {ql.x, ql.y, ql.z, ql.w};
+                const uint32_t hw[4] = {qh.x, qh.y, qh.z, qh.w};
+                int slo = 0, shi = 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    uint32_t lo = (lw[k] & 0x0F0F0F0Fu) | (((hw[k] >> sh_lo) & 0x03030303u) << 4);
+                    uint32_t hi = ((lw[k] >> 4) & 0x0F0F0F0Fu) | (((hw[k] >> sh_hi) & 0x03030303u) << 4);
+                    slo = dot4(lo, ylw[k], slo);
+                    shi = dot4(hi, yhw[k], shi);
+                }
+                // unsigned 6-bit values: subtract 32 * sum(y) per 16-group.
+                sumi = sc_at(is_lo) * (slo - 32 * bslo) + sc_at(is_hi) * (shi - 32 * bshi);
+                dd = f16_to_f32(drow[r][sbc]) * yd;
+            }
+            // exact integer reduction over the 8 parts of the super-block
+            sumi += shfl_xor(sumi, 1);
+            sumi += shfl_xor(sumi, 2);
+            sumi += shfl_xor(sumi, 4);
+            float term;
+            if (KIND == AOTK_Q6_K) {
+                term = dd * (float)sumi;
+            } else {
+                summ += shfl_xor(summ, 1);
+                summ += shfl_xor(summ, 2);
+                summ += shfl_xor(summ, 4);
+                term = dd * (float)sumi - dm * (float)summ;
+            }
+            // sequential fold over the super-blocks of this step
+            const int nstep = nb - sb0 < 8 ? nb - sb0 : 8;
+            float s_acc = acc[r];
+            for (int gg = 0; gg < nstep; gg++) s_acc = s_acc + readlane_f(term, gg * 8);
+            acc[r] = s_acc;
+        }
+    }
+    if (lane == 0) {
+        for (int r = 0; r < R; r++)
+            if (rvalid[r]) store_row(a, grow0 + r, tok, acc[r]);
+    }
+}
+
+// ------------------------------------------------------ Q8_0 / Q4_0 / Q5_0
+// Wave = 8 rows. Phase A: lanes turn 32 blocks of 2 rows per pass into the 8
+// per-lane integer sums P and the scale D = f16(d) * y.d, staged in LDS.
+// Phase B: lane (row r, chain l) runs acc_l = fma(D, P_l, acc_l) in block
+// order. Then the avx2 horizontal sum.
+constexpr int Q80_STEP = 32;
+
+template <int KIND>
+__global__ __launch_bounds__(256) void k_mv_q80(MvArgs a) {
+    __shared__ float sP[4][8][Q80_STEP][8];
+    __shared__ float sD[4][8][Q80_STEP];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int tok = blockIdx.y;
+    const int grow0 = (blockIdx.x * 4 + wave) * 8;
+    const int nb = a.nb;
+    const int8_t *xq = a.xq + (size_t)tok * a.cols;
+    const float *xd = a.xd + (size_t)tok * nb;
+    float acc = 0.0f;
+    const int rb_row = lane >> 3, chain = lane & 7;
+
+    for (int i0 = 0; i0 < nb; i0 += Q80_STEP) {
+        for (int pass = 0; pass < 4; pass++) {
+            const int rr = 2 * pass + (lane >> 5);
+            const int bi = i0 + (lane & 31);
+            const int grow = grow0 + rr;
+            float P[8];
+            float D = 0.0f;
+            for (int l = 0; l < 8; l++) P[l] = 0.0f;
+            if (grow < a.total_rows && bi < nb) {
+                int local;
+                int s = seg_of(a, grow, local);
+                const size_t blk = (size_t)local * nb + bi;
+                const uint4 y0 = *(const uint4 *)(xq + (size_t)bi * 32);
+                const uint4 y1 = *(const uint4 *)(xq + (size_t)bi * 32 + 16);
+                const uint32_t yw[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+                const float dw = f16_to_f32(((const uint16_t *)a.w1[s])[blk]);
+                D = dw * xd[bi];
+                if (KIND == AOTK_Q8_0) {
+                    const uint4 w0 = *(const uint4 *)(a.w[s] + blk * 32);
+                    const uint4 w1 = *(const uint4 *)(a.w[s] + blk * 32 + 16);
+                    const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                    for (int l = 0; l < 8; l++) P[l] = (float)dot4(ww[l], yw[l], 0);
+                } else {
+                    const uint4 w0 = *(const uint4 *)(a.w[s] + blk * 16);
+                    const uint32_t nw[4] = {w0.x, w0.y, w0.z, w0.w};
+                    uint32_t qh = 0;
+                    if (KIND == AOTK_Q5_0) qh = ((const uint32_t *)a.w2[s])[blk];
+                    for (int l = 0; l < 8; l++) {
+                        uint32_t v = l < 4 ? (nw[l] & 0x0F0F0F0Fu) : ((nw[l - 4] >> 4) & 0x0F0F0F0Fu);
+                        int off;
+                        if (KIND == AOTK_Q5_0) {
+                            uint32_t b4 = (qh >> (4 * l)) & 0xFu;
+                            uint32_t spread = (b4 & 1u) | ((b4 & 2u) << 7) | ((b4 & 4u) << 14) | ((b4 & 8u) << 21);
+                            v |= spread << 4;
+                            off = dot4(0xF0F0F0F0u, yw[l], 0);  // -16 * sum(y)
+                        } else {
+                            off = dot4(0xF8F8F8F8u, yw[l], 0);  // -8 * sum(y)
+                        }
+                        P[l] = (float)dot4(v, yw[l], off);
+                    }
+                }
+            }
+            float *dst = &sP[wave][rr][lane & 31][0];
+            *(float4 *)dst = make_float4(P[0], P[1], P[2], P[3]);
+            *(float4 *)(dst + 4) = make_float4(P[4], P[5], P[6], P[7]);
+            sD[wave][rr][lane & 31] = D;
+        }
+        __syncthreads();
+        const int nstep = nb - i0 < Q80_STEP ? nb - i0 : Q80_STEP;
+        for (int ii = 0; ii < nstep; ii++) acc = fmaf(sD[wave][rb_row][ii], sP[wave][rb_row][ii][chain], acc);
+        __syncthreads();
+    }
+    // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7))  (simd_avx2.rs:27-34)
+    float t = acc + shfl_xor(acc, 4);
+    float u = t + shfl_xor(t, 2);
+    float v = u + shfl_xor(u, 1);
+    const int grow = grow0 + rb_row;
+    if (chain == 0 && grow < a.total_rows) store_row(a, grow, tok, v);
+}
+
+// ------------------------------------------------------- F16 / BF16 / F32
+template <int KIND>
+__device__ __forceinline__ float wval(const uint8_t *row, size_t i) {
+    if (KIND == AOTK_F32) return ((const float *)row)[i];
+    uint32_t h = ((const uint16_t *)row)[i];
+    if (KIND == AOTK_BF16) return bf16_to_f32(h);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void k_mv_float(MvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int tok = blockIdx.y;
+    const int r8 = lane >> 3, l = lane & 7;
+    const int grow = (blockIdx.x * 4 + wave) * 8 + r8;
+    const bool valid = grow < a.total_rows;
+    int local;
+    const int s = seg_of(a, valid ? grow : 0, local);
+    const uint8_t *row = a.w[s] + (size_t)local * a.rb;
+    const float *x = a.xf + (size_t)tok * a.cols;
+    const size_t n8 = a.cols / 8;
+    float acc = 0.0f;
+    if (valid) {
+        size_t sI = 0;
+        for (; sI + 4 <= n8; sI += 4) {
+            float w0 = wval<KIND>(row, 8 * sI + l), w1 = wval<KIND>(row, 8 * (sI + 1) + l);
+            float w2 = wval<KIND>(row, 8 * (sI + 2) + l), w3 = wval<KIND>(row, 8 * (sI + 3) + l);
+            float x0 = x[8 * sI + l], x1 = x[8 * (sI + 1) + l], x2 = x[8 * (sI + 2) + l], x3 = x[8 * (sI + 3) + l];
+            acc = fmaf(w0, x0, acc);
+            acc = fmaf(w1, x1, acc);
+            acc = fmaf(w2, x2, acc);
+            acc = fmaf(w3, x3, acc);
+        }
+        for (; sI < n8; sI++) acc = fmaf(wval<KIND>(row, 8 * sI + l), x[8 * sI + l], acc);
+    }
+    float t = acc + shfl_xor(acc, 4);
+    float u = t + shfl_xor(t, 2);
+    float v = u + shfl_xor(u, 1);
+    if (l == 0 && valid) {
+        for (size_t i = n8 * 8; i < a.cols; i++) v = v + wval<KIND>(row, i) * x[i];
+        store_row(a, grow, tok, v);
+    }
+}
+
+// ----------------------------------------------------------------- launch
+
+static MvArgs make_args(int n, const DevWeight *const ws[], float *const ys[], const float *const adds[], const void *x_act) {
+    MvArgs a = {};
+    const DevWeight &w0 = *ws[0];
+    a.nseg = n;
+    a.total_rows = 0;
+    for (int i = 0; i < n; i++) {
+        a.w[i] = ws[i]->plane[0];
+        a.w1[i] = ws[i]->plane[1];
+        a.w2[i] = ws[i]->plane[2];
+        a.y[i] = ys[i];
+        a.add[i] = adds ? adds[i] : nullptr;
+        a.rows[i] = (int)ws[i]->rows;
+        a.total_rows += (int)ws[i]->rows;
+    }
+    a.nb = (int)w0.nb;
+    a.rb = row_bytes(w0.kind, w0.cols);
+    a.cols = w0.cols;
+    int act = activation(w0.kind);
+    if (act == ACT_Q8_K) {
+        ActQ8K q = *(const ActQ8K *)x_act;
+        a.xq = q.qs;
+        a.xd = q.d;
+        a.xbs = q.bsums;
+    } else if (act == ACT_Q8_0) {
+        ActQ8_0 q = *(const ActQ8_0 *)x_act;
+        a.xq = q.qs;
+        a.xd = q.d;
+    } else {
+        a.xf = (const float *)x_act;
+    }
+    return a;
+}
+
+static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
+    dim3 grid;
+    grid.y = (unsigned)m;
+    switch (kind) {
+    case AOTK_Q4_K:
+        grid.x = (unsigned)((a.total_rows + 7) / 8);
+        k_mv_kquant<AOTK_Q4_K, 2><<<grid, 256, 0, s>>>(a);
+        break;
+    case AOTK_Q5_K:
+        grid.x = (unsigned)((a.total_rows + 7) / 8);
+        k_mv_kquant<AOTK_Q5_K, 2><<<grid, 256, 0, s>>>(a);
+        break;
+    case AOTK_Q6_K:
+        grid.x = (unsigned)((a.total_rows + 7) / 8);
+        k_mv_kquant<AOTK_Q6_K, 2><<<grid, 256, 0, s>>>(a);
+        break;
+    case AOTK_Q8_0:
+        grid.x = (unsigned)((a.total_rows + 31) / 32);
+        k_mv_q80<AOTK_Q8_0><<<grid, 256, 0, s>>>(a);
+        break;
+    case AOTK_Q4_0:
+        grid.x = (unsigned)((a.total_rows + 31) / 32);
+        k_mv_q80<AOTK_Q4_0><<<grid, 256, 0, s>>>(a);
+        break;
+    case AOTK_Q5_0:
+        grid.x = (unsigned)((a.total_rows + 31) / 32);
+        k_mv_q80<AOTK_Q5_0><<<grid, 256, 0, s>>>(a);
+        break;
+    case AOTK_F16:
+        grid.x = (unsigned)((a.total_rows + 31) / 32);
+        k_mv_float<AOTK_F16><<<grid, 256, 0, s>>>(a);
+        break;
+    case AOTK_BF16:
+        grid.x = (unsigned)((a.total_rows + 31) / 32);
+        k_mv_float<AOTK_BF16><<<grid, 256, 0, s>>>(a);
+        break;
+    default:
+        grid.x = (unsigned)((a.total_rows + 31) / 32);
+        k_mv_float<AOTK_F32><<<grid, 256, 0, s>>>(a);
+        break;
+    }
+}
+
+void launch_matvec(const DevWeight &w, const void *x_act, size_t m, float *y, const float *add, hipStream_t s) {
+    const DevWeight *ws[1] = {&w};
+    float *ys[1] = {y};
+    const float *adds[1] = {add};
+    MvArgs a = make_args(1, ws, ys, adds, x_act);
+    launch_args(w.kind, a, m, s);
+}
+
+void launch_matvec_multi(int n, const DevWeight *const ws[], float *const ys[], const void *x_act, hipStream_t s) {
+    MvArgs a = make_args(n, ws, ys, nullptr, x_act);
+    launch_args(ws[0]->kind, a, 1, s);
+}
+
+}  // namespace aotk

@@ -1,0 +1,269 @@
+/*
+ * aotk.h - C ABI of the MI355X (gfx950) implementation of aot-llm's quantized
+ * inference hot path.
+ *
+ * Everything here is plain C: pointers, sizes and POD structs, no C++ or torch
+ * types. A Rust FFI crate (the reference's intended caller) binds it with
+ * `extern "C"` declarations; Python binds it with ctypes (aot-llm_amd/aotk).
+ *
+ * Conventions (mirroring crates/aot-kernels/src/capi.rs:129-141 and
+ * crates/aot-codegen/src/aot_llm.h:56-62):
+ *   - every entry point returns 0 on success and -1 on failure (pointer
+ *     returning calls return NULL), and the reason is available from
+ *     aotk_last_error() (thread-local string);
+ *   - calls are synchronous with respect to the host unless documented
+ *     otherwise; all device work is issued on the library's own HIP stream;
+ *   - the library is single-threaded per model/state, like the reference's
+ *     `&mut Gpu` handle (crates/aot-kernels/src/metal.rs:331-520) and the
+ *     `Model.lock` serialisation of aot_eval (capi.rs:181, :485).
+ *
+ * Pointers named *_dev are device (HBM) addresses allocated with
+ * aotk_dev_alloc (or any hipMalloc'd memory of the same device).
+ */
+#ifndef AOTK_H
+#define AOTK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Formats                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Weight element kinds: crates/aot-kernels/src/quant.rs:35-87 (`Kind`). */
+enum aotk_kind {
+    AOTK_F32 = 0,
+    AOTK_F16 = 1,
+    AOTK_BF16 = 2,
+    AOTK_Q4_0 = 3,
+    AOTK_Q5_0 = 4,
+    AOTK_Q8_0 = 5,
+    AOTK_Q4_K = 6,
+    AOTK_Q5_K = 7,
+    AOTK_Q6_K = 8,
+    AOTK_KIND_NONE = -1
+};
+
+/* Activation blocks, byte-compatible with the reference's #[repr(C)]
+ * structs: BlockQ8_0 (quant.rs:194-199, 36 bytes) and BlockQ8_K
+ * (quant.rs:210-216, 292 bytes). */
+typedef struct aotk_block_q8_0 {
+    float d;
+    int8_t qs[32];
+} aotk_block_q8_0;
+
+typedef struct aotk_block_q8_k {
+    float d;
+    int8_t qs[256];
+    int16_t bsums[16];
+} aotk_block_q8_k;
+
+/* One tensor of the weight blob: crates/aot-kernels/src/state.rs:165-180
+ * (`Tensor {kind, off, len, rows, cols}`). kind == AOTK_KIND_NONE marks an
+ * absent optional tensor. Matrices are row-major, `rows` outputs x `cols`
+ * inputs (ggml order), rows are `row_bytes(kind, cols)` apart. */
+typedef struct aotk_tensor {
+    int32_t kind;
+    int32_t reserved;
+    uint64_t off;
+    uint64_t len;
+    uint64_t rows;
+    uint64_t cols;
+} aotk_tensor;
+
+/* Hyper-parameters: crates/aot-kernels/src/state.rs:126-161 (`Dims`). */
+typedef struct aotk_dims {
+    uint64_t dim, hidden, n_layer, n_head, n_kv_head, head_dim, rot_dim, vocab, n_ctx_train;
+    float eps, rope_base, rope_scale;
+    uint32_t swa_window;
+    float rope_base_local, rope_scale_local;
+} aotk_dims;
+
+/* Architecture switches: crates/aot-codegen/src/model.rs:152-192
+ * (`ArchFlags`; fused_qkv/fused_gate_up are row views resolved by the
+ * caller into separate tensors, model.rs:352-363). */
+typedef struct aotk_flags {
+    uint8_t rope_neox, qkv_bias, qk_norm, embd_scale, post_norms, gelu;
+    uint8_t reserved[2];
+    uint32_t swa_pattern;
+} aotk_flags;
+
+/* Per-layer tensors: crates/aot-codegen/src/model.rs:121-148 (`LayerSpec`). */
+typedef struct aotk_layer {
+    aotk_tensor attn_norm, wq, wk, wv, wo, ffn_norm, gate, up, down;
+    aotk_tensor bq, bk, bv, q_norm, k_norm, attn_post_norm, ffn_post_norm;
+    int32_t local_attn;
+    int32_t reserved;
+} aotk_layer;
+
+/* The model graph: what aot-codegen bakes into the generated model.rs as
+ * DIMS / TOKEN_EMBD / OUTPUT_NORM / OUTPUT / LAYERS (emit.rs:399-464). */
+typedef struct aotk_model_spec {
+    aotk_dims dims;
+    aotk_flags flags;
+    aotk_tensor token_embd, output_norm;
+    aotk_tensor output;     /* kind NONE: tied to token_embd (emit.rs:421-424) */
+    aotk_tensor rope_freqs; /* kind NONE: no per-dimension factors */
+    const aotk_layer *layers; /* dims.n_layer entries */
+} aotk_model_spec;
+
+/* ------------------------------------------------------------------------ */
+/* Library / device                                                          */
+/* ------------------------------------------------------------------------ */
+
+/* Last error of the calling thread (capi.rs:129-141 `aot_last_error`). */
+const char *aotk_last_error(void);
+
+/* Select the device and create the library stream. Idempotent. */
+int aotk_init(int device);
+
+/* Device memory helpers (so C/Rust/Python callers need no HIP headers). */
+void *aotk_dev_alloc(size_t bytes);
+int aotk_dev_free(void *ptr_dev);
+int aotk_h2d(void *dst_dev, const void *src_host, size_t bytes);
+int aotk_d2h(void *dst_host, const void *src_dev, size_t bytes);
+int aotk_memset(void *dst_dev, int value, size_t bytes);
+int aotk_sync(void);
+
+/* Bytes per row of `cols` elements (quant.rs:70-73 `Kind::row_bytes`). */
+size_t aotk_row_bytes(int kind, size_t cols);
+
+/* ------------------------------------------------------------------------ */
+/* Weights in HBM                                                            */
+/* ------------------------------------------------------------------------ */
+
+typedef struct aotk_weight aotk_weight;
+
+/* Upload one row-major quantized matrix (`w: &[u8]` of the reference's
+ * matvec_* entry points, matvec.rs:358-401) to HBM. The bytes are repacked
+ * on the device into the library's aligned plane layout (same byte count). */
+aotk_weight *aotk_weight_upload(int kind, const void *bytes_host, size_t rows, size_t cols);
+/* Same, from bytes already in device memory (not retained). */
+aotk_weight *aotk_weight_from_dev(int kind, const void *bytes_dev, size_t rows, size_t cols);
+int aotk_weight_free(aotk_weight *w);
+
+/* Dequantize rows [row0, row0+n_rows) into out_dev (n_rows*cols floats):
+ * quant.rs:300-443 (`dequant_row_*`), bit-exact. */
+int aotk_dequant_rows(const aotk_weight *w, size_t row0, size_t n_rows, float *out_dev);
+
+/* Reference weight encoders on the device: quantize.rs:282-294
+ * (`quantize_row`), applied to every row of x_dev (rows*cols floats);
+ * writes rows*row_bytes bytes in the reference (GGUF) layout. Bit-exact. */
+int aotk_quantize_rows(int kind, const float *x_dev, size_t rows, size_t cols, void *out_dev);
+
+/* ------------------------------------------------------------------------ */
+/* Activation quantizers (quant.rs:231-283)                                  */
+/* ------------------------------------------------------------------------ */
+
+/* `quantize_q8_0(x, out)`: n % 32 == 0, out has n/32 blocks. */
+int aotk_quantize_q8_0(const float *x_dev, size_t n, aotk_block_q8_0 *out_dev);
+/* `quantize_q8_k(x, out)`: n % 256 == 0, out has n/256 blocks. */
+int aotk_quantize_q8_k(const float *x_dev, size_t n, aotk_block_q8_k *out_dev);
+
+/* ------------------------------------------------------------------------ */
+/* Matrix-vector / matrix-matrix products (matvec.rs:358-583)                */
+/* ------------------------------------------------------------------------ */
+
+/* `matvec_<kind>(pool, out, w, x, rows, cols)` with a pre-quantized input:
+ * x_dev holds cols/32 aotk_block_q8_0 (Q4_0/Q5_0/Q8_0 weights),
+ * cols/256 aotk_block_q8_k (Q4_K/Q5_K/Q6_K) or cols floats (F16/BF16/F32).
+ * out_dev[r] = dot(row r, x). Bit-exact with the reference's avx2+f16c
+ * kernel set (simd_avx2.rs). */
+int aotk_matvec(const aotk_weight *w, const void *x_dev, float *out_dev);
+
+/* Same, with an f32 input vector that is first quantized on the device to
+ * the weight's activation format (the generated forward's
+ * `quantize_q8_k(&s.xb..); matvec_q4_k(..)` pair, emit.rs:131-140). */
+int aotk_matvec_f32(const aotk_weight *w, const float *x_dev, float *out_dev);
+
+/* `matmul_<kind>(pool, out, w, xs, m, rows, cols)` (matvec.rs:524-546):
+ * m input vectors back to back in xs_dev (same formats as aotk_matvec),
+ * out_dev[i*rows + r]. Bit-identical to m calls of aotk_matvec. */
+int aotk_matmul(const aotk_weight *w, const void *xs_dev, size_t m, float *out_dev);
+
+/* ------------------------------------------------------------------------ */
+/* Transformer operators (ops.rs)                                            */
+/* ------------------------------------------------------------------------ */
+
+/* rmsnorm over m rows of n: ops.rs:7-18, :361-366. */
+int aotk_rmsnorm(float *out_dev, const float *x_dev, const float *w_dev, size_t n, size_t m, float eps);
+/* rmsnorm_heads in place: ops.rs:74-87. */
+int aotk_rmsnorm_heads(float *x_dev, const float *w_dev, size_t n_heads, size_t head_dim, float eps);
+/* rope / rope_neox in place over m rows, cs_dev holds m rows of rot_dim
+ * interleaved (cos, sin): ops.rs:40-70, :377-391. */
+int aotk_rope(float *x_dev, size_t m, size_t n_heads, size_t head_dim, size_t rot_dim, const float *cs_dev, int neox);
+/* In-place softmax of n values: ops.rs:98-112. */
+int aotk_softmax(float *x_dev, size_t n);
+/* h = silu(h)*up / gelu(h)*up: ops.rs:115-134. */
+int aotk_silu_mul(float *h_dev, const float *up_dev, size_t n);
+int aotk_gelu_mul(float *h_dev, const float *up_dev, size_t n);
+/* x += y: ops.rs:145-148. */
+int aotk_add(float *x_dev, const float *y_dev, size_t n);
+/* Causal GQA attention for m query rows at positions pos0..pos0+m-1 over a
+ * [n_layer][ctx][kv_dim] f32 cache: ops.rs:185-218 (`attention`, m == 1) and
+ * ops.rs:517-556 (`attention_rows`). window 0 = full attention. */
+int aotk_attention(float *out_dev, const float *q_dev, const float *k_cache_dev, const float *v_cache_dev,
+                   size_t n_head, size_t n_kv_head, size_t head_dim, size_t ctx, size_t layer,
+                   size_t pos0, size_t m, size_t window);
+/* First index of the strict maximum: sampler.rs:99-109. */
+int aotk_argmax(const float *x_dev, size_t n, uint32_t *out_host);
+
+/* ------------------------------------------------------------------------ */
+/* Whole model: the generated forward()/forward_batch() (emit.rs:466-516)    */
+/* ------------------------------------------------------------------------ */
+
+typedef struct aotk_model aotk_model;
+typedef struct aotk_state aotk_state;
+
+/* Upload the tensor-data blob (the `.incbin` weight section, emit.rs:707-795)
+ * to HBM once and build the device tensor table. The spec is copied. */
+aotk_model *aotk_model_load(const aotk_model_spec *spec, const void *blob_host, size_t blob_len);
+/* Build the model's weights directly in HBM from the synthetic generator
+ * (seeded N(0, 0.02)-shaped values, norms 1 + N(0, 0.02)) and the device
+ * encoders; the result is byte-identical to encoding the same values with
+ * the reference's quantize_row on the host. */
+aotk_model *aotk_model_synthetic(const aotk_model_spec *spec, uint64_t seed);
+/* Copy the model's blob (reference layout) back to the host. */
+int aotk_model_download(const aotk_model *model, void *blob_host, size_t blob_len);
+int aotk_model_free(aotk_model *model);
+/* HBM bytes read by one decode step's weight matrices (incl. lm-head). */
+uint64_t aotk_model_weight_bytes(const aotk_model *model);
+
+/* Activation buffers + KV cache resident in HBM: state.rs:251-355
+ * (`State::new(ctx, max_batch)`). The RoPE tables for every position are
+ * computed on the host with libm once, exactly like rope_cos_sin
+ * (ops.rs:28-34), and uploaded. */
+aotk_state *aotk_state_new(aotk_model *model, size_t ctx, size_t max_batch);
+int aotk_state_free(aotk_state *state);
+
+/* One decode step (`ForwardFn`, app.rs:32-62; emitted `forward`,
+ * emit.rs:466-486). Errors (not panics) on token >= vocab or pos >= ctx. */
+int aotk_forward(aotk_state *state, uint32_t token, size_t pos, int want_logits);
+/* One batched prompt step of 1..max_batch tokens (`ForwardBatchFn`;
+ * emit.rs:491-516); logits of the last token only. */
+int aotk_forward_batch(aotk_state *state, const uint32_t *tokens_host, size_t m, size_t pos0, int want_logits);
+/* Copy the vocab logits to the host. */
+int aotk_logits(aotk_state *state, float *out_host);
+/* Greedy token of the current logits (sampler.rs:99-109). */
+int aotk_greedy(aotk_state *state, uint32_t *token_out);
+/* Greedy generation: starting from the current logits (after the prompt),
+ * emit n tokens as app.rs:553-610 does with temperature 0 (sample, then feed
+ * back unless it was the last), positions pos, pos+1, ... Writes the n
+ * token ids to tokens_host. Device-resident loop: only token ids cross PCIe. */
+int aotk_generate_greedy(aotk_state *state, size_t pos, size_t n, uint32_t *tokens_host);
+/* KV rows [0, n_pos) of every layer to / from the host, laid out as the
+ * reference's cache: [n_layer][n_pos][kv_dim] f32 for K, then the same for V. */
+int aotk_kv_download(aotk_state *state, size_t n_pos, float *k_host, float *v_host);
+int aotk_kv_upload(aotk_state *state, size_t n_pos, const float *k_host, const float *v_host);
+/* The library's HIP stream (hipStream_t) for callers that time on it. */
+void *aotk_stream(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AOTK_H */
