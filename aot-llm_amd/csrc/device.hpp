@@ -124,3 +124,39 @@ __device__ __forceinline__ float synth_value(uint64_t seed, uint32_t tensor_inde
 }
 
 }  // namespace aotk
+
+#include "libm_match.h"
+#include "libm_tables.h"
+
+namespace aotk {
+
+__device__ __constant__ static const uint32_t expf_exc[][2] = {AOTK_EXPF_EXC_DATA};
+__device__ __constant__ static const uint32_t tanhf_exc[][2] = {AOTK_TANHF_EXC_DATA};
+
+__device__ __forceinline__ bool exc_lookup(const uint32_t (*tab)[2], int n, uint32_t key, uint32_t &out) {
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        int mid = (lo + hi) >> 1;
+        if (tab[mid][0] < key) lo = mid + 1;
+        else hi = mid;
+    }
+    if (lo < n && tab[lo][0] == key) {
+        out = tab[lo][1];
+        return true;
+    }
+    return false;
+}
+
+// expf / tanhf bit-identical to the host libm the reference links against.
+__device__ __forceinline__ float aotk_expf(float x) {
+    uint32_t o;
+    if (AOTK_EXPF_EXC_N && exc_lookup(expf_exc, AOTK_EXPF_EXC_N, __float_as_uint(x), o)) return __uint_as_float(o);
+    return lm_expf(x);
+}
+__device__ __forceinline__ float aotk_tanhf(float x) {
+    uint32_t o;
+    if (AOTK_TANHF_EXC_N && exc_lookup(tanhf_exc, AOTK_TANHF_EXC_N, __float_as_uint(x), o)) return __uint_as_float(o);
+    return lm_tanhf(x);
+}
+
+}  // namespace aotk

@@ -5,8 +5,10 @@
 //   bias + rmsnorm_heads + rope + store_kv in one per-head kernel,
 //   GQA decode attention split over position chunks (K/V rows read once),
 //   argmax over the vocabulary.
-// Reductions run as fixed-shape trees (deterministic run to run); they differ
-// from the reference's sequential f32 sums by rounding only.
+// Every float sum that feeds an activation quantizer runs in the reference's
+// sequential order (a different order changes results by an ulp, which flips
+// int8 roundings downstream); transcendental functions are the host-libm
+// matched aotk_expf / aotk_tanhf. Maxima and integer sums use trees.
 #include "device.hpp"
 #include "formats.hpp"
 #include "internal.hpp"
@@ -33,6 +35,24 @@ __device__ float block_sum(float v, float *red) {
     float t = lane < nw ? red[lane] : 0.0f;
     t = wave_sum(t);
     return t;
+}
+
+// ss = sum of v*v over n values in LDS, in index order (ops.rs:10-13). Run
+// by one thread; the result is broadcast through LDS.
+__device__ float seq_sumsq_lds(const float *v, int n, float *bcast) {
+    if (threadIdx.x == 0) {
+        float ss = 0.0f;
+        for (int i = 0; i < n; i += 4) {
+            float4 q = *(const float4 *)(v + i);
+            ss += q.x * q.x;
+            ss += q.y * q.y;
+            ss += q.z * q.z;
+            ss += q.w * q.w;
+        }
+        *bcast = ss;
+    }
+    __syncthreads();
+    return *bcast;
 }
 
 // Quantize 256 values held 4 per lane (element 4*lane + k) of one wave into
@@ -108,16 +128,17 @@ __device__ __forceinline__ ActQ8_0 q80_row(ActQ8_0 a, size_t row, size_t n) {
 // n % 256 == 0, n <= 8192 (the normalised row is staged in LDS).
 __global__ __launch_bounds__(1024) void k_rmsnorm_quant(const float *__restrict__ x, const float *__restrict__ w, int n,
                                                          float eps, RmsOut out) {
-    __shared__ float row[8192];
-    __shared__ float red[16];
+    __shared__ __align__(16) float row[8192];
+    __shared__ float bc;
     const size_t m = blockIdx.x;
     const float *xr = x + m * n;
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) ss += xr[i] * xr[i];
-    ss = block_sum(ss, red);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) row[i] = xr[i];
+    __syncthreads();
+    float ss = seq_sumsq_lds(row, n, &bc);
     float r = 1.0f / sqrtf(ss / (float)n + eps);
+    __syncthreads();
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float v = xr[i] * r * w[i];
+        float v = row[i] * r * w[i];
         row[i] = v;
         if (out.f32) out.f32[m * n + i] = v;
     }
@@ -154,10 +175,10 @@ void launch_quant_f32(const float *x, size_t n, size_t m, RmsOut out, hipStream_
 }
 
 // silu_mul / gelu_mul (ops.rs:115-134) then quantization; one wave per 256.
-__device__ __forceinline__ float silu_f(float v, float b) { return v / (1.0f + expf(-v)) * b; }
+__device__ __forceinline__ float silu_f(float v, float b) { return v / (1.0f + aotk_expf(-v)) * b; }
 __device__ __forceinline__ float gelu_f(float v) {
     const float k = (float)1.1283791670955126 / (float)1.4142135623730951;
-    return 0.5f * v * (1.0f + tanhf(k * (v + 0.044715f * v * v * v)));
+    return 0.5f * v * (1.0f + aotk_tanhf(k * (v + 0.044715f * v * v * v)));
 }
 
 __global__ void k_glu_quant(const float *__restrict__ gate, const float *__restrict__ up, int n, size_t total_blk, int gelu,
@@ -207,7 +228,7 @@ void launch_embed(const DevWeight &embd, const uint32_t *tokens, size_t m, float
 // store_kv copy into the cache (ops.rs:152-157). Heads [0, n_head) are q,
 // [n_head, n_head + n_kv_head) are k (+ v).
 __global__ __launch_bounds__(64) void k_qkv_post(QkvPost p, size_t pos0, const int *pos_dev) {
-    __shared__ float hv[256];
+    __shared__ __align__(16) float hv[256];
     const int lane = threadIdx.x;
     const size_t i = blockIdx.y;
     const int hh = blockIdx.x;
@@ -226,9 +247,8 @@ __global__ __launch_bounds__(64) void k_qkv_post(QkvPost p, size_t pos0, const i
     }
     __syncthreads();
     if (nw) {
-        float ss = 0.0f;
-        for (int e = lane; e < hd; e += 64) ss += hv[e] * hv[e];
-        ss = wave_sum(ss);
+        __shared__ float bc;
+        float ss = seq_sumsq_lds(hv, hd, &bc);
         float r = 1.0f / sqrtf(ss / (float)hd + p.eps);
         for (int e = lane; e < hd; e += 64) hv[e] = hv[e] * r * nw[e];
         __syncthreads();
@@ -266,118 +286,139 @@ void launch_qkv_post(const QkvPost &p, size_t m, size_t pos0, const int *pos_dev
 }
 
 // ----------------------------------------------------------- attention
-// Causal GQA attention (ops.rs:185-218, :517-556) as split-position flash
-// decoding: block (kv head, chunk of ATT_CH positions, query row) scores its
-// chunk for the gqa query heads sharing the kv head (each K/V row is read once
-// for all of them), keeps (max, sum, unnormalised output); a second kernel
-// merges the chunks.
+// Causal GQA attention (ops.rs:185-218 `attention`, :517-556
+// `attention_rows`) in the reference's arithmetic order, in three passes:
+//   1. scores: one thread per cached position computes q.k sequentially over
+//      the head dimension for every query head of the kv group (each K row is
+//      read once for the group), times 1/sqrt(hd);
+//   2. softmax per (row, head): max, host-libm exp, a sequential sum in
+//      position order, multiply by 1/sum (ops.rs:98-112);
+//   3. output: one thread per (head, dim) accumulates p_t * v_t in position
+//      order (ops.rs:209-215); V rows are read coalesced across dims.
+// Scratch: probabilities [m][n_head][span].
 constexpr int ATT_CH = 64;
 constexpr int ATT_MAX_GQA = 8;
 
 struct AttnArgs {
     float *out;
     const float *q, *k_cache, *v_cache;
-    float *ws_ml;  // [m][n_head][n_chunks][2]
-    float *ws_o;   // [m][n_head][n_chunks][hd]
-    int n_head, n_kv_head, hd, n_chunks;
+    float *prob;
+    int n_head, n_kv_head, hd, span;
     size_t pos0, window;
     const int *pos_dev;
     float scale;
 };
 
+__device__ __forceinline__ void row_range(const AttnArgs &a, size_t i, size_t &t0, size_t &n) {
+    size_t pos = a.pos_dev ? (size_t)*a.pos_dev : a.pos0 + i;
+    n = pos + 1;
+    t0 = (a.window > 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
+}
+
 template <int HD>
-__global__ __launch_bounds__(64) void k_attn_chunk(AttnArgs a) {
-    constexpr int E = HD / 64;  // output dims per lane
+__global__ __launch_bounds__(64) void k_attn_scores(AttnArgs a) {
     __shared__ float sq[ATT_MAX_GQA][HD];
-    __shared__ float sp[ATT_MAX_GQA][ATT_CH];
     const int lane = threadIdx.x;
     const int kvh = blockIdx.x, c = blockIdx.y;
     const size_t i = blockIdx.z;
     const int gqa = a.n_head / a.n_kv_head;
-    const size_t pos = a.pos_dev ? (size_t)*a.pos_dev : a.pos0 + i;
-    const size_t n = pos + 1;
-    const size_t t0 = (a.window > 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
+    size_t t0, n;
+    row_range(a, i, t0, n);
     const size_t start = t0 + (size_t)c * ATT_CH;
-    const size_t kv = (size_t)a.n_kv_head * HD;
-    const size_t q_dim = (size_t)a.n_head * HD;
-    const size_t slot = (i * a.n_head + (size_t)kvh * gqa) * a.n_chunks + c;  // head kvh*gqa + h at + h*n_chunks
-    if (start >= n) {
-        for (int h = 0; h < gqa; h++)
-            if (lane < 2) a.ws_ml[(slot + (size_t)h * a.n_chunks) * 2 + lane] = lane == 0 ? -INFINITY : 0.0f;
-        return;
-    }
-    const int cnt = (int)((n - start) < (size_t)ATT_CH ? (n - start) : (size_t)ATT_CH);
+    if (start >= n) return;
+    const size_t kv = (size_t)a.n_kv_head * HD, q_dim = (size_t)a.n_head * HD;
     for (int h = 0; h < gqa; h++)
         for (int e = lane; e < HD; e += 64) sq[h][e] = a.q[i * q_dim + (size_t)(kvh * gqa + h) * HD + e];
     __syncthreads();
-    // scores: lane = position
-    float sc[ATT_MAX_GQA];
-    for (int h = 0; h < gqa; h++) sc[h] = -INFINITY;
-    if (lane < cnt) {
-        const float4 *kr = (const float4 *)(a.k_cache + (start + lane) * kv + (size_t)kvh * HD);
-        float acc[ATT_MAX_GQA];
-        for (int h = 0; h < gqa; h++) acc[h] = 0.0f;
-        for (int d4 = 0; d4 < HD / 4; d4++) {
-            float4 k4 = kr[d4];
-            for (int h = 0; h < gqa; h++) {
-                const float *qq = &sq[h][4 * d4];
-                acc[h] += qq[0] * k4.x + qq[1] * k4.y + qq[2] * k4.z + qq[3] * k4.w;
-            }
-        }
-        for (int h = 0; h < gqa; h++) sc[h] = acc[h] * a.scale;
-    }
-    float mh[ATT_MAX_GQA], lh[ATT_MAX_GQA];
-    for (int h = 0; h < gqa; h++) {
-        mh[h] = wave_max(sc[h]);
-        float e = lane < cnt ? expf(sc[h] - mh[h]) : 0.0f;
-        sp[h][lane] = e;
-        lh[h] = wave_sum(e);
-    }
-    __syncthreads();
-    // output: lane owns dims lane + 64*k
-    float o[ATT_MAX_GQA][E];
-    for (int h = 0; h < gqa; h++)
-        for (int k = 0; k < E; k++) o[h][k] = 0.0f;
-    for (int t = 0; t < cnt; t++) {
-        const float *vr = a.v_cache + (start + t) * kv + (size_t)kvh * HD;
-        float vv[E];
-        for (int k = 0; k < E; k++) vv[k] = vr[lane + 64 * k];
+    const size_t t = start + lane;
+    if (t >= n) return;
+    const float4 *kr = (const float4 *)(a.k_cache + t * kv + (size_t)kvh * HD);
+    float acc[ATT_MAX_GQA];
+    for (int h = 0; h < gqa; h++) acc[h] = 0.0f;
+    for (int d4 = 0; d4 < HD / 4; d4++) {
+        float4 k4 = kr[d4];
         for (int h = 0; h < gqa; h++) {
-            float pw = sp[h][t];
-            for (int k = 0; k < E; k++) o[h][k] += pw * vv[k];
+            const float *qq = &sq[h][4 * d4];
+            float s = acc[h];
+            s += qq[0] * k4.x;
+            s += qq[1] * k4.y;
+            s += qq[2] * k4.z;
+            s += qq[3] * k4.w;
+            acc[h] = s;
         }
     }
-    for (int h = 0; h < gqa; h++) {
-        size_t sl = slot + (size_t)h * a.n_chunks;
-        if (lane == 0) {
-            a.ws_ml[sl * 2] = mh[h];
-            a.ws_ml[sl * 2 + 1] = lh[h];
-        }
-        for (int k = 0; k < E; k++) a.ws_o[sl * HD + lane + 64 * k] = o[h][k];
-    }
+    for (int h = 0; h < gqa; h++)
+        a.prob[(i * a.n_head + (size_t)(kvh * gqa + h)) * a.span + (t - t0)] = acc[h] * a.scale;
 }
 
-__global__ void k_attn_merge(AttnArgs a) {
+__global__ __launch_bounds__(256) void k_attn_softmax(AttnArgs a) {
+    __shared__ float red[4];
+    __shared__ float bc;
     const int h = blockIdx.x;
     const size_t i = blockIdx.y;
-    const int d = threadIdx.x;
-    const size_t base = (i * a.n_head + h) * a.n_chunks;
-    float M = -INFINITY;
-    for (int c = 0; c < a.n_chunks; c++) M = fmaxf(M, a.ws_ml[(base + c) * 2]);
-    float L = 0.0f, o = 0.0f;
-    for (int c = 0; c < a.n_chunks; c++) {
-        float mc = a.ws_ml[(base + c) * 2];
-        if (mc == -INFINITY) continue;
-        float f = expf(mc - M);
-        L += a.ws_ml[(base + c) * 2 + 1] * f;
-        o += a.ws_o[(base + c) * a.hd + d] * f;
+    size_t t0, n;
+    row_range(a, i, t0, n);
+    const int cnt = (int)(n - t0);
+    float *p = a.prob + (i * a.n_head + h) * a.span;
+    float mx = -INFINITY;
+    for (int t = threadIdx.x; t < cnt; t += blockDim.x) mx = fmaxf(mx, p[t]);
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int t = threadIdx.x; t < cnt; t += blockDim.x) p[t] = aotk_expf(p[t] - mx);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float sum = 0.0f;
+        int t = 0;
+        for (; t + 4 <= cnt; t += 4) {
+            float4 e = *(const float4 *)(p + t);
+            sum += e.x;
+            sum += e.y;
+            sum += e.z;
+            sum += e.w;
+        }
+        for (; t < cnt; t++) sum += p[t];
+        bc = 1.0f / sum;
     }
-    a.out[i * (size_t)a.n_head * a.hd + (size_t)h * a.hd + d] = o / L;
+    __syncthreads();
+    const float inv = bc;
+    for (int t = threadIdx.x; t < cnt; t += blockDim.x) p[t] = p[t] * inv;
+}
+
+// Block = 64 output dims of one head of one row.
+__global__ __launch_bounds__(64) void k_attn_out(AttnArgs a) {
+    const int hd = a.hd;
+    const int per_head = hd / 64;
+    const int h = blockIdx.x / per_head, d = (blockIdx.x % per_head) * 64 + threadIdx.x;
+    const size_t i = blockIdx.y;
+    const int gqa = a.n_head / a.n_kv_head;
+    const int kvh = h / gqa;
+    size_t t0, n;
+    row_range(a, i, t0, n);
+    const int cnt = (int)(n - t0);
+    const size_t kv = (size_t)a.n_kv_head * hd;
+    const float *p = a.prob + (i * a.n_head + h) * a.span;
+    const float *vp = a.v_cache + t0 * kv + (size_t)kvh * hd + d;
+    float o = 0.0f;
+    int t = 0;
+    for (; t + 8 <= cnt; t += 8) {
+        float v[8], w[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            v[k] = vp[(size_t)(t + k) * kv];
+            w[k] = p[t + k];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) o += w[k] * v[k];
+    }
+    for (; t < cnt; t++) o += p[t] * vp[(size_t)t * kv];
+    a.out[i * (size_t)a.n_head * hd + (size_t)h * hd + d] = o;
 }
 
 size_t attention_scratch_bytes(size_t n_head, size_t head_dim, size_t ctx, size_t m) {
-    size_t n_chunks = (ctx + ATT_CH - 1) / ATT_CH;
-    return align_up(m * n_head * n_chunks * 2 * 4, 256) + align_up(m * n_head * n_chunks * head_dim * 4, 256);
+    (void)head_dim;
+    return align_up(m * n_head * align_up(ctx, 4) * 4, 256);
 }
 
 void launch_attention(float *out, const float *q, const float *k_cache, const float *v_cache, size_t n_head,
@@ -389,11 +430,8 @@ void launch_attention(float *out, const float *q, const float *k_cache, const fl
     a.q = q;
     a.k_cache = k_cache;
     a.v_cache = v_cache;
-    // chunks: enough for the longest row (positions up to ctx_rows)
-    size_t span = window > 0 && window < ctx_rows ? window : ctx_rows;
-    a.n_chunks = (int)((span + ATT_CH - 1) / ATT_CH);
-    a.ws_ml = scratch;
-    a.ws_o = (float *)((uint8_t *)scratch + align_up(m * n_head * a.n_chunks * 2 * 4, 256));
+    a.prob = scratch;
+    a.span = (int)align_up(ctx_rows, 4);
     a.n_head = (int)n_head;
     a.n_kv_head = (int)n_kv_head;
     a.hd = (int)head_dim;
@@ -401,13 +439,15 @@ void launch_attention(float *out, const float *q, const float *k_cache, const fl
     a.window = window;
     a.pos_dev = pos_dev;
     a.scale = 1.0f / sqrtf((float)head_dim);
-    dim3 grid((unsigned)n_kv_head, (unsigned)a.n_chunks, (unsigned)m);
+    size_t span = window > 0 && window < ctx_rows ? window : ctx_rows;
+    dim3 grid((unsigned)n_kv_head, (unsigned)((span + ATT_CH - 1) / ATT_CH), (unsigned)m);
     switch (head_dim) {
-    case 64: k_attn_chunk<64><<<grid, 64, 0, s>>>(a); break;
-    case 128: k_attn_chunk<128><<<grid, 64, 0, s>>>(a); break;
-    default: k_attn_chunk<256><<<grid, 64, 0, s>>>(a); break;
+    case 64: k_attn_scores<64><<<grid, 64, 0, s>>>(a); break;
+    case 128: k_attn_scores<128><<<grid, 64, 0, s>>>(a); break;
+    default: k_attn_scores<256><<<grid, 64, 0, s>>>(a); break;
     }
-    k_attn_merge<<<dim3((unsigned)n_head, (unsigned)m), (unsigned)head_dim, 0, s>>>(a);
+    k_attn_softmax<<<dim3((unsigned)n_head, (unsigned)m), 256, 0, s>>>(a);
+    k_attn_out<<<dim3((unsigned)(n_head * head_dim / 64), (unsigned)m), 64, 0, s>>>(a);
 }
 
 // ------------------------------------------------------------ elementwise
@@ -422,15 +462,16 @@ void launch_add(float *x, const float *y, size_t n, hipStream_t s) {
 
 // Gemma post-norm join: x += rmsnorm(y) (emit.rs:320-324).
 __global__ __launch_bounds__(1024) void k_rmsnorm_add(float *x, const float *y, const float *w, int n, float eps) {
-    __shared__ float red[16];
+    __shared__ __align__(16) float row[8192];
+    __shared__ float bc;
     const size_t m = blockIdx.x;
     const float *yr = y + m * n;
     float *xr = x + m * n;
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) ss += yr[i] * yr[i];
-    ss = block_sum(ss, red);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) row[i] = yr[i];
+    __syncthreads();
+    float ss = seq_sumsq_lds(row, n, &bc);
     float r = 1.0f / sqrtf(ss / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) xr[i] = xr[i] + yr[i] * r * w[i];
+    for (int i = threadIdx.x; i < n; i += blockDim.x) xr[i] = xr[i] + row[i] * r * w[i];
 }
 void launch_rmsnorm_add(float *x, const float *y, const float *w, size_t n, size_t m, float eps, hipStream_t s) {
     k_rmsnorm_add<<<(unsigned)m, 1024, 0, s>>>(x, y, w, (int)n, eps);
@@ -445,25 +486,26 @@ void launch_silu_mul(float *h, const float *up, size_t n, int gelu, hipStream_t 
     k_silu_mul<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(h, up, n, gelu);
 }
 
+// softmax (ops.rs:98-112) of one vector: max, exp, sequential sum, scale.
 __global__ __launch_bounds__(1024) void k_softmax(float *x, int n) {
     __shared__ float red[16];
+    __shared__ float bc;
     float mx = -INFINITY;
     for (int i = threadIdx.x; i < n; i += blockDim.x) mx = fmaxf(mx, x[i]);
     mx = wave_max(mx);
-    __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
     __syncthreads();
     float t = (threadIdx.x & 63) < (blockDim.x >> 6) ? red[threadIdx.x & 63] : -INFINITY;
     mx = wave_max(t);
-    float sum = 0.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float e = expf(x[i] - mx);
-        x[i] = e;
-        sum += e;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) x[i] = aotk_expf(x[i] - mx);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float sum = 0.0f;
+        for (int i = 0; i < n; i++) sum += x[i];
+        bc = 1.0f / sum;
     }
     __syncthreads();
-    sum = block_sum(sum, red);
-    float inv = 1.0f / sum;
+    float inv = bc;
     for (int i = threadIdx.x; i < n; i += blockDim.x) x[i] = x[i] * inv;
 }
 void launch_softmax(float *x, size_t n, hipStream_t s) { k_softmax<<<1, 1024, 0, s>>>(x, (int)n); }

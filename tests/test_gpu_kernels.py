@@ -1,0 +1,165 @@
+"""Per-kernel parity of the HIP path against the CPU oracle (bit-exact for
+integer / dequantization / quantized-dot work, tolerance for float ops)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+F32, F16, BF16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = range(9)
+ALL = [F32, F16, BF16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K]
+NAMES = dict(zip(ALL, ["f32", "f16", "bf16", "q4_0", "q5_0", "q8_0", "q4_K", "q5_K", "q6_K"]))
+
+
+def cols_for(kind):
+    return {F32: [8, 64, 2053, 4096], F16: [8, 64, 2053, 4096], BF16: [12, 64, 2053],
+            Q4_0: [32, 96, 2048, 5632], Q5_0: [32, 96, 2048], Q8_0: [32, 96, 2048, 12288],
+            Q4_K: [256, 512, 2048, 5632], Q5_K: [256, 512, 2560], Q6_K: [256, 512, 2048, 5632]}[kind]
+
+
+def weights(kind, rows, cols, seed, oracle):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    return oracle.quantize_rows(kind, w)
+
+
+@pytest.mark.parametrize("kind", ALL, ids=lambda k: NAMES[k])
+def test_encoder_and_dequant_bitexact(aotk, oracle, kind):
+    rng = np.random.default_rng(kind + 1)
+    for cols in cols_for(kind)[:3]:
+        x = (rng.standard_normal((37, cols)) * 0.5).astype(np.float32)
+        ref = oracle.quantize_rows(kind, x)
+        got = aotk.quantize_rows(kind, x)
+        assert np.array_equal(ref, got), f"{NAMES[kind]} cols={cols}: device encoder differs"
+        w = aotk.Weight(kind, ref, 37, cols)
+        deq = aotk.dequant_rows(w)
+        ref_deq = oracle.dequant_rows(kind, ref, cols)
+        assert np.array_equal(deq.view(np.uint32), ref_deq.view(np.uint32)), f"{NAMES[kind]} dequant differs"
+
+
+def test_f16_all_halves(aotk, oracle):
+    h = np.arange(65536, dtype=np.uint16)
+    w = aotk.Weight(F16, h.view(np.uint8), 1, 65536)
+    got = aotk.dequant_rows(w)[0]
+    ref = oracle.dequant_rows(F16, h.view(np.uint8), 65536)[0]
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_activation_quantizers(aotk, oracle):
+    rng = np.random.default_rng(5)
+    for n in (256, 2048, 5632):
+        x = (rng.standard_normal(n) * 3).astype(np.float32)
+        x[7] = -x[3] if n > 256 else x[7]  # magnitude tie: first index wins
+        x[512 % n:512 % n + 256] = 0.0  # an all-zero block
+        a = aotk.quantize_q8_k(x)
+        b = oracle.quantize_q8_k(x)
+        assert a.tobytes() == b.tobytes()
+        a0 = aotk.quantize_q8_0(x)
+        b0 = oracle.quantize_q8_0(x)
+        assert a0.tobytes() == b0.tobytes()
+
+
+@pytest.mark.parametrize("kind", ALL, ids=lambda k: NAMES[k])
+def test_matvec_bitexact(aotk, oracle, kind):
+    rng = np.random.default_rng(100 + kind)
+    for cols in cols_for(kind):
+        rows = 67
+        raw = weights(kind, rows, cols, kind * 7 + cols, oracle)
+        x = (rng.standard_normal(cols) * 2).astype(np.float32)
+        act = oracle.quantize_act(kind, x)
+        ref = oracle.matvec(kind, raw, act, rows, cols)
+        w = aotk.Weight(kind, raw, rows, cols)
+        got = aotk.matvec(w, act)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), \
+            f"{NAMES[kind]} cols={cols}: max diff {np.abs(got - ref).max()}"
+        got2 = aotk.matvec_f32(w, x)
+        assert np.array_equal(got2.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", [Q4_K, Q6_K, Q8_0, Q5_K, F16], ids=lambda k: NAMES[k])
+def test_matmul_equals_matvec(aotk, oracle, kind):
+    rng = np.random.default_rng(7)
+    cols, rows = 512, 37
+    raw = weights(kind, rows, cols, 3, oracle)
+    w = aotk.Weight(kind, raw, rows, cols)
+    for m in (1, 3, 4, 7, 9):
+        xs = [(rng.standard_normal(cols)).astype(np.float32) for _ in range(m)]
+        acts = np.concatenate([oracle.quantize_act(kind, x) for x in xs])
+        got = aotk.matmul(w, acts, m)
+        ref = oracle.matmul(kind, raw, acts, m, rows, cols).reshape(m, rows)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_rope_bitexact(aotk, oracle):
+    rng = np.random.default_rng(9)
+    for neox in (0, 1):
+        x = rng.standard_normal(4 * 128).astype(np.float32)
+        cs = rng.standard_normal(128).astype(np.float32)
+        got = aotk.rope(x, 1, 4, 128, 128, cs, neox)
+        ref = x.copy()
+        oracle.load().or_rope(oracle.ptr(ref), 4, 128, 128, oracle.ptr(cs), neox)
+        assert np.array_equal(got, ref)
+
+
+def test_rmsnorm_softmax_glu(aotk, oracle):
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((3, 2048)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(2048)).astype(np.float32)
+    got = aotk.rmsnorm(x, w, 1e-5)
+    ref = np.stack([_or_rmsnorm(oracle, r, w) for r in x])
+    assert np.array_equal(got, ref)
+    s = rng.standard_normal(1000).astype(np.float32) * 4
+    ref = s.copy()
+    oracle.load().or_softmax(oracle.ptr(ref), ref.size)
+    assert np.array_equal(aotk.softmax(s), ref)
+    h, up = rng.standard_normal(4096).astype(np.float32), rng.standard_normal(4096).astype(np.float32)
+    for fn, name in ((aotk.silu_mul, "or_silu_mul"), (aotk.gelu_mul, "or_gelu_mul")):
+        ref = h.copy()
+        getattr(oracle.load(), name)(oracle.ptr(ref), oracle.ptr(up), ref.size)
+        assert np.array_equal(fn(h, up), ref)
+
+
+def _or_rmsnorm(oracle, x, w):
+    out = np.empty_like(x)
+    oracle.load().or_rmsnorm(oracle.ptr(out), oracle.ptr(np.ascontiguousarray(x)), oracle.ptr(w), x.size, 1e-5)
+    return out
+
+
+@pytest.mark.parametrize("hd,nh,nkv,window", [(64, 32, 4, 0), (128, 32, 8, 0), (256, 8, 4, 5), (128, 4, 4, 0)])
+def test_attention(aotk, oracle, hd, nh, nkv, window):
+    rng = np.random.default_rng(hd + nh)
+    ctx, layer = 150, 1
+    kv = nkv * hd
+    kc = rng.standard_normal(2 * ctx * kv).astype(np.float32)
+    vc = rng.standard_normal(2 * ctx * kv).astype(np.float32)
+    for pos0, m in ((0, 1), (1, 1), (63, 1), (64, 1), (149, 1), (10, 7), (100, 50)):
+        q = rng.standard_normal(m * nh * hd).astype(np.float32)
+        got = aotk.attention(q, kc, vc, nh, nkv, hd, ctx, layer, pos0, m, window)
+        ref = np.zeros(m * nh * hd, np.float32)
+        p = oracle.Pool(4)
+        oracle.load().or_attention(p.p, oracle.ptr(ref), oracle.ptr(q), oracle.ptr(kc), oracle.ptr(vc), nh, nkv, hd, ctx,
+                                   layer, pos0, m, window)
+        assert np.array_equal(got, ref), (pos0, m, np.abs(got - ref).max())
+
+
+def test_argmax(aotk, oracle):
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(128256).astype(np.float32)
+    assert aotk.argmax(x) == oracle.argmax(x)
+    x[5000] = x[90000] = 100.0  # tie: first index wins
+    assert aotk.argmax(x) == 5000
+    x[3] = np.nan
+    assert aotk.argmax(x) == 5000
+    assert aotk.argmax(np.full(1000, -np.inf, np.float32)) == 0
+
+
+def test_libm_matched_exp_tanh(aotk, oracle):
+    """silu/gelu through the device expf/tanhf against glibc over a wide range."""
+    rng = np.random.default_rng(3)
+    h = np.concatenate([rng.standard_normal(100000) * 10, np.linspace(-100, 100, 100000),
+                        [0.0, -0.0, 1e-30, -1e-30, 88.7, -104.0, 32.564632415771484, 63.1]]).astype(np.float32)
+    up = np.ones_like(h)
+    for fn, name in ((aotk.silu_mul, "or_silu_mul"), (aotk.gelu_mul, "or_gelu_mul")):
+        ref = h.copy()
+        getattr(oracle.load(), name)(oracle.ptr(ref), oracle.ptr(up), ref.size)
+        got = fn(h, up)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), name

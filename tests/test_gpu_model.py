@@ -1,0 +1,83 @@
+"""Whole-model parity: the HIP forward against the oracle's emitted forward."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TINY = ["tiny-llama", "tiny-qwen2", "tiny-qwen3", "tiny-gemma3", "tiny-q4km", "tiny-q8_0", "tiny-q5km"]
+
+
+def rel_l2(a, b):
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.mark.parametrize("name", TINY)
+def test_synthetic_weights_bitexact(aotk, oracle, name):
+    from aotk import configs
+    spec = configs.build(name)
+    blob = oracle.synth_blob(spec, 0x5EED)
+    m = aotk.Model(spec, seed=0x5EED)
+    assert np.array_equal(m.download(), blob)
+
+
+@pytest.mark.parametrize("name", TINY)
+def test_forward_logits_and_greedy(aotk, oracle, name):
+    from aotk import configs
+    spec = configs.build(name)
+    blob = oracle.synth_blob(spec, 0x5EED)
+    ctx = 48
+    ref = oracle.Model(spec, blob, ctx)
+    gm = aotk.Model(spec, blob)
+    st = aotk.State(gm, ctx)
+    toks = configs.prompt_tokens(7, 9, spec.d["vocab"])
+    ref.prompt(toks)
+    st.prompt(toks)
+    a, b = st.logits(), ref.logits()
+    assert rel_l2(a, b) < 1e-3, rel_l2(a, b)
+    assert np.array_equal(a, b), f"logits not bit-exact (rel L2 {rel_l2(a, b):.3g})"
+    assert int(np.argmax(a)) == oracle.argmax(b)
+    n = 16
+    assert st.generate(len(toks), n) == ref.generate(len(toks), n)
+
+
+@pytest.mark.parametrize("name", ["tiny-llama", "tiny-gemma3"])
+def test_batch_matches_single(aotk, oracle, name):
+    from aotk import configs
+    spec = configs.build(name)
+    gm = aotk.Model(spec, seed=3)
+    toks = configs.prompt_tokens(3, 12, spec.d["vocab"])
+    s1, s2 = aotk.State(gm, 32), aotk.State(gm, 32)
+    s1.prompt(toks, batch=64)
+    for i, t in enumerate(toks):
+        s2.forward(t, i, i + 1 == len(toks))
+    assert np.array_equal(s1.logits(), s2.logits())
+
+
+def test_errors(aotk):
+    from aotk import configs
+    spec = configs.build("tiny-llama")
+    gm = aotk.Model(spec, seed=1)
+    st = aotk.State(gm, 8, 4)
+    with pytest.raises(aotk.AotkError, match="out of range"):
+        st.forward(10 ** 6, 0)
+    with pytest.raises(aotk.AotkError, match="exceeds the context"):
+        st.forward(1, 8)
+    with pytest.raises(aotk.AotkError, match="batch size"):
+        st.forward_batch([1] * 5, 0)
+
+
+def test_tinyllama_config_greedy_stream(aotk, oracle):
+    """TinyLlama shape Q4_K_M, 6-token prompt, 32 greedy tokens."""
+    from aotk import configs
+    spec = configs.build("tinyllama-1.1b-q4km")
+    gm = aotk.Model(spec, seed=0x5EED)
+    blob = gm.download()
+    toks = configs.prompt_tokens(1, 6, spec.d["vocab"])
+    ctx = 38
+    st = aotk.State(gm, ctx)
+    st.prompt(toks)
+    ref = oracle.Model(spec, blob, ctx)
+    ref.prompt(toks)
+    assert rel_l2(st.logits(), ref.logits()) < 1e-3
+    assert np.array_equal(st.logits(), ref.logits())
+    assert st.generate(6, 32) == ref.generate(6, 32)
