@@ -145,6 +145,7 @@ def load(path=None):
     _sig(lib, "aotk_kv_download", i, [vp, sz, fp, fp])
     _sig(lib, "aotk_kv_upload", i, [vp, sz, fp, fp])
     _sig(lib, "aotk_stream", vp, [])
+    _sig(lib, "aotk_time_matvec", i, [C.POINTER(vp), sz, vp, sz, C.POINTER(C.c_float)])
     _lib = lib
     return lib
 

@@ -90,6 +90,16 @@ class Weight:
             pass
 
 
+def time_matvec(weights, x, iters):
+    """Mean device ms per matvec launch, rotating over `weights` (same kind
+    and shape), timed with HIP events on the library stream."""
+    dx = DeviceBuffer.from_numpy(np.ascontiguousarray(x, np.float32))
+    arr = (C.c_void_p * len(weights))(*[w.h for w in weights])
+    ms = C.c_float()
+    abi.check(_lib().aotk_time_matvec(arr, len(weights), dx.ptr, iters, C.byref(ms)))
+    return ms.value
+
+
 def dequant_rows(w, row0=0, n_rows=None):
     n_rows = w.rows - row0 if n_rows is None else n_rows
     out = DeviceBuffer(n_rows * w.cols * 4)

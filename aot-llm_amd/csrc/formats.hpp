@@ -31,38 +31,38 @@ __device__ __forceinline__ float dequant_elem(const WView &w, size_t r, size_t c
         return (float)(v - 16) * d;
     }
     if (KIND == AOTK_Q4_K || KIND == AOTK_Q5_K) {
-        constexpr int TS = KIND == AOTK_Q4_K ? 144 : 176;
-        const uint8_t *b = w.p0 + r * w.rb + (c / 256) * TS;
+        const uint8_t *rowp = w.p0 + r * w.rb;
+        const size_t sb = c / 256, nb = w.nb;
+        auto B = [&](int off) { return rowp[kq_off(off, sb, nb)]; };
         int e = (int)(c % 256);
         int j = e / 64, hi = (e % 64) / 32, l = e % 32;
-        const uint32_t *h = (const uint32_t *)b;
+        const uint32_t *h = (const uint32_t *)(rowp + kq_off(0, sb, nb));  // bytes [0,16) are one chunk
         float d = f16_to_f32(h[0] & 0xFFFF), dmin = f16_to_f32(h[0] >> 16);
         int sc, m;
         scale_min_k4(2 * j + hi, h[1], h[2], h[3], sc, m);
         float d1 = d * (float)sc, m1 = dmin * (float)m;
         int q;
         if (KIND == AOTK_Q4_K) {
-            uint8_t qb = b[16 + 32 * j + l];
+            uint8_t qb = B(16 + 32 * j + l);
             q = hi ? (qb >> 4) : (qb & 0xF);
         } else {
-            uint8_t qb = b[48 + 32 * j + l];
+            uint8_t qb = B(48 + 32 * j + l);
             q = hi ? (qb >> 4) : (qb & 0xF);
-            if (b[16 + l] & (1u << (2 * j + hi))) q += 16;
+            if (B(16 + l) & (1u << (2 * j + hi))) q += 16;
         }
         return d1 * (float)q - m1;
     }
     // Q6_K
-    size_t blk = r * w.nb + c / 256;
-    const uint8_t *b = w.p0 + blk * 208;
+    const size_t sb = c / 256, nb = w.nb, blk = r * nb + sb;
+    const uint8_t *rowp = w.p0 + r * nb * 208;
+    auto B = [&](int off) { return rowp[kq_off(off, sb, nb)]; };
     float d = f16_to_f32(((const uint16_t *)w.p1)[blk]);
     int e = (int)(c % 256);
     int n = e / 128, t = e % 128, quarter = t / 32, l = t % 32;
-    const uint8_t *ql = b + 64 * n, *qh = b + 128 + 32 * n;
-    const int8_t *sc = (const int8_t *)(b + 192 + 8 * n);
-    int lo = (quarter & 1) ? ql[l + 32] : ql[l];
+    int lo = (quarter & 1) ? B(64 * n + l + 32) : B(64 * n + l);
     lo = (quarter >= 2) ? (lo >> 4) : (lo & 0xF);
-    int q = (lo | (((qh[l] >> (2 * quarter)) & 3) << 4)) - 32;
-    return d * (float)sc[l / 16 + 2 * quarter] * (float)q;
+    int q = (lo | (((B(128 + 32 * n + l) >> (2 * quarter)) & 3) << 4)) - 32;
+    return d * (float)(int8_t)B(192 + 8 * n + l / 16 + 2 * quarter) * (float)q;
 }
 
 

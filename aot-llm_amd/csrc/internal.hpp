@@ -89,12 +89,19 @@ inline ActQ8_0 act_q8_0_view(void *base, size_t n, size_t rows) {
 
 // A weight matrix in HBM in the library's plane layout (same byte count as
 // the reference layout; planes are 256-byte aligned):
-//   Q4_K, Q5_K, F16, BF16, F32: the reference rows unchanged (row-major);
-//   Q6_K: plane0 = per block 208 bytes (ql, qh, scales), plane1 = f16 d;
+//   F16, BF16, F32: the reference rows unchanged (row-major);
+//   Q4_K, Q5_K: row-major rows, each stored chunk-major: the super-block's
+//     bytes [16k, 16k+16) of super-block s at row offset (k*nb + s)*16, so
+//     that the 16-byte chunk k of consecutive super-blocks is contiguous;
+//   Q6_K: plane0 = the first 208 bytes (ql, qh, scales) of each super-block,
+//     chunk-major per row like Q4_K; plane1 = f16 d per super-block;
 //   Q8_0: plane0 = 32 quants per block, plane1 = f16 d;
 //   Q4_0: plane0 = 16 nibble bytes per block, plane1 = f16 d;
 //   Q5_0: plane0 = 16 nibble bytes, plane1 = f16 d, plane2 = u32 qh.
-// Block (r, b) of a plane lives at index r * nb + b.
+// Block (r, b) of a block plane lives at index r * nb + b.
+
+// Chunk-major row offset of byte `off` of super-block s (K-quants).
+__host__ __device__ inline size_t kq_off(size_t off, size_t s, size_t nb) { return ((off >> 4) * nb + s) * 16 + (off & 15); }
 struct DevWeight {
     int kind;
     size_t rows, cols, nb;

@@ -15,6 +15,7 @@
 #include "device.hpp"
 #include "internal.hpp"
 
+
 namespace aotk {
 
 constexpr int MAX_SEG = 3;
@@ -56,9 +57,52 @@ __device__ __forceinline__ void store_row(const MvArgs &a, int grow, int tok, fl
 }
 
 // --------------------------------------------------------------- K-quants
+// Rows of more than 64 super-blocks (cols > 16384).
 // Wave = R rows. Lane = 8*g + p: super-block slot g (8 per step), part p
-// (32 of the block's 256 values). Integer sums are reduced over the 8 lanes of
+// (32 of the block's 256 values). Each step's loads (activation slice, and per
+// row the block header and 16 quant bytes, plus the high bits) are issued
+// one step ahead of their use. Integer sums are reduced over the 8 lanes of
 // a slot, then the per-super-block f32 terms are folded in order.
+template <int KIND, int R>
+struct KqLoads {
+    uint4 ylo, yhi;
+    float yd;
+    int bslo, bshi;
+    uint4 a[R];  // Q4_K/Q5_K: header;   Q6_K: ql
+    uint4 q[R];  // Q4_K/Q5_K: quants;   Q6_K: qh
+    uint4 h[R];  // Q5_K: qh;            Q6_K: scales 8n..8n+7 (x, y used)
+    float d6[R]; // Q6_K: d
+};
+
+template <int KIND, int R>
+__device__ __forceinline__ void kq_load(KqLoads<KIND, R> &L, const uint8_t *const wrow[R], const uint16_t *const drow[R],
+                                        int nb, const int8_t *xq, const float *xd, const int16_t *xbs, int sbc, int p, int y_lo,
+                                        int y_hi, int bs_lo, int bs_hi) {
+    L.ylo = *(const uint4 *)(xq + (size_t)sbc * 256 + y_lo);
+    L.yhi = *(const uint4 *)(xq + (size_t)sbc * 256 + y_hi);
+    L.yd = xd[sbc];
+    L.bslo = xbs[(size_t)sbc * 16 + bs_lo];
+    L.bshi = xbs[(size_t)sbc * 16 + bs_hi];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint8_t *b = wrow[r] + (size_t)sbc * 16;  // chunk-major rows
+        const size_t cs = (size_t)nb * 16;                // stride of one chunk index
+        if (KIND == AOTK_Q4_K || KIND == AOTK_Q5_K) {
+            constexpr int QC = KIND == AOTK_Q4_K ? 1 : 3;
+            L.a[r] = *(const uint4 *)b;
+            L.q[r] = *(const uint4 *)(b + (QC + p) * cs);
+            if (KIND == AOTK_Q5_K) L.h[r] = *(const uint4 *)(b + (1 + (p & 1)) * cs);
+        } else {
+            const int n = p >> 2, half = (p >> 1) & 1, which = p & 1;
+            L.a[r] = *(const uint4 *)(b + (4 * n + 2 * which + half) * cs);
+            L.q[r] = *(const uint4 *)(b + (8 + 2 * n + half) * cs);
+            uint2 sc = *(const uint2 *)(b + 12 * cs + 8 * n);
+            L.h[r] = make_uint4(sc.x, sc.y, 0, 0);
+            L.d6[r] = f16_to_f32(drow[r][sbc]);
+        }
+    }
+}
+
 template <int KIND, int R>
 __global__ __launch_bounds__(256) void k_mv_kquant(MvArgs a) {
     const int lane = threadIdx.x & 63;
@@ -75,6 +119,7 @@ __global__ __launch_bounds__(256) void k_mv_kquant(MvArgs a) {
     const uint8_t *wrow[R];
     const uint16_t *drow[R];
     bool rvalid[R];
+#pragma unroll
     for (int r = 0; r < R; r++) {
         int grow = grow0 + r;
         rvalid[r] = grow < a.total_rows;
@@ -89,6 +134,7 @@ __global__ __launch_bounds__(256) void k_mv_kquant(MvArgs a) {
         }
     }
     float acc[R];
+#pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.0f;
 
     // lane-constant geometry
@@ -107,37 +153,30 @@ __global__ __launch_bounds__(256) void k_mv_kquant(MvArgs a) {
         bs_hi = bs_lo + 2;
     }
 
+    KqLoads<KIND, R> cur;
+    kq_load<KIND, R>(cur, wrow, drow, nb, xq, xd, xbs, g < nb ? g : nb - 1, p, y_lo, y_hi, bs_lo, bs_hi);
     for (int sb0 = 0; sb0 < nb; sb0 += 8) {
-        const int sb = sb0 + g;
-        const bool valid = sb < nb;
-        const int sbc = valid ? sb : nb - 1;
-        const uint4 ylo = *(const uint4 *)(xq + (size_t)sbc * 256 + y_lo);
-        const uint4 yhi = *(const uint4 *)(xq + (size_t)sbc * 256 + y_hi);
-        const float yd = xd[sbc];
-        const int bslo = xbs[(size_t)sbc * 16 + bs_lo];
-        const int bshi = xbs[(size_t)sbc * 16 + bs_hi];
-        const uint32_t ylw[4] = {ylo.x, ylo.y, ylo.z, ylo.w};
-        const uint32_t yhw[4] = {yhi.x, yhi.y, yhi.z, yhi.w};
-
+        KqLoads<KIND, R> nxt;
+        const bool more = sb0 + 8 < nb;
+        if (more) {
+            const int sbn = sb0 + 8 + g;
+            kq_load<KIND, R>(nxt, wrow, drow, nb, xq, xd, xbs, sbn < nb ? sbn : nb - 1, p, y_lo, y_hi, bs_lo, bs_hi);
+        }
+        const uint32_t ylw[4] = {cur.ylo.x, cur.ylo.y, cur.ylo.z, cur.ylo.w};
+        const uint32_t yhw[4] = {cur.yhi.x, cur.yhi.y, cur.yhi.z, cur.yhi.w};
+        const int nstep = nb - sb0 < 8 ? nb - sb0 : 8;
+#pragma unroll
         for (int r = 0; r < R; r++) {
             int sumi = 0, summ = 0;
-            float dd = 0.0f, dm = 0.0f;
+            float dd, dm = 0.0f;
             if (KIND == AOTK_Q4_K || KIND == AOTK_Q5_K) {
-                constexpr int TS = KIND == AOTK_Q4_K ? 144 : 176;
-                constexpr int QS = KIND == AOTK_Q4_K ? 16 : 48;
-                const uint8_t *b = wrow[r] + (size_t)sbc * TS;
-                const uint4 hdr = *(const uint4 *)b;
-                const uint4 q = *(const uint4 *)(b + QS + 16 * p);
-                const int j = p >> 1, h = p & 1;
+                const uint4 hdr = cur.a[r];
+                const int j = p >> 1;
                 int sc_lo, m_lo, sc_hi, m_hi;
                 scale_min_k4(2 * j, hdr.y, hdr.z, hdr.w, sc_lo, m_lo);
                 scale_min_k4(2 * j + 1, hdr.y, hdr.z, hdr.w, sc_hi, m_hi);
-                const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-                uint32_t hw[4] = {0, 0, 0, 0};
-                if (KIND == AOTK_Q5_K) {
-                    const uint4 qh = *(const uint4 *)(b + 16 + 16 * h);
-                    hw[0] = qh.x; hw[1] = qh.y; hw[2] = qh.z; hw[3] = qh.w;
-                }
+                const uint32_t qw[4] = {cur.q[r].x, cur.q[r].y, cur.q[r].z, cur.q[r].w};
+                const uint32_t hw[4] = {cur.h[r].x, cur.h[r].y, cur.h[r].z, cur.h[r].w};
                 int slo = 0, shi = 0;
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
@@ -151,24 +190,19 @@ __global__ __launch_bounds__(256) void k_mv_kquant(MvArgs a) {
                     shi = dot4(hi, yhw[k], shi);
                 }
                 sumi = sc_lo * slo + sc_hi * shi;
-                summ = m_lo * bslo + m_hi * bshi;
-                dd = f16_to_f32(hdr.x & 0xFFFFu) * yd;
-                dm = f16_to_f32(hdr.x >> 16) * yd;
+                summ = m_lo * cur.bslo + m_hi * cur.bshi;
+                dd = f16_to_f32(hdr.x & 0xFFFFu) * cur.yd;
+                dm = f16_to_f32(hdr.x >> 16) * cur.yd;
             } else {  // Q6_K
-                const int n = p >> 2, half = (p >> 1) & 1, which = p & 1;
-                const uint8_t *b = wrow[r] + (size_t)sbc * 208;
-                const uint4 ql = *(const uint4 *)(b + 64 * n + 32 * which + 16 * half);
-                const uint4 qh = *(const uint4 *)(b + 128 + 32 * n + 16 * half);
-                const uint32_t scw = *(const uint32_t *)(b + 192 + 8 * n);  // sc[8n .. 8n+3]
-                const uint32_t scw2 = *(const uint32_t *)(b + 192 + 8 * n + 4);
-                const int is_lo = half + 2 * which, is_hi = is_lo + 4;  // index within sc[8n..8n+8]
-                auto sc_at = [&](int i) -> int {
-                    uint32_t w = i < 4 ? scw : scw2;
-                    return (int)(int8_t)((w >> (8 * (i & 3))) & 0xFFu);
-                };
+                const int half = (p >> 1) & 1, which = p & 1;
+                const int is_lo = half + 2 * which, is_hi = is_lo + 4;
+                const uint32_t scw = is_lo < 4 ? cur.h[r].x : cur.h[r].y;
+                const uint32_t scw2 = cur.h[r].y;
+                const int sc_lo = (int)(int8_t)((scw >> (8 * (is_lo & 3))) & 0xFFu);
+                const int sc_hi = (int)(int8_t)((scw2 >> (8 * (is_hi & 3))) & 0xFFu);
                 const int sh_lo = 2 * which, sh_hi = 4 + 2 * which;
-                const uint32_t lw[4] = {ql.x, ql.y, ql.z, ql.w};
-                const uint32_t hw[4] = {qh.x, qh.y, qh.z, qh.w};
+                const uint32_t lw[4] = {cur.a[r].x, cur.a[r].y, cur.a[r].z, cur.a[r].w};
+                const uint32_t hw[4] = {cur.q[r].x, cur.q[r].y, cur.q[r].z, cur.q[r].w};
                 int slo = 0, shi = 0;
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
@@ -178,8 +212,8 @@ __global__ __launch_bounds__(256) void k_mv_kquant(MvArgs a) {
                     shi = dot4(hi, yhw[k], shi);
                 }
                 // unsigned 6-bit values: subtract 32 * sum(y) per 16-group.
-                sumi = sc_at(is_lo) * (slo - 32 * bslo) + sc_at(is_hi) * (shi - 32 * bshi);
-                dd = f16_to_f32(drow[r][sbc]) * yd;
+                sumi = sc_lo * (slo - 32 * cur.bslo) + sc_hi * (shi - 32 * cur.bshi);
+                dd = cur.d6[r] * cur.yd;
             }
             // exact integer reduction over the 8 parts of the super-block
             sumi += shfl_xor(sumi, 1);
@@ -195,15 +229,172 @@ __global__ __launch_bounds__(256) void k_mv_kquant(MvArgs a) {
                 term = dd * (float)sumi - dm * (float)summ;
             }
             // sequential fold over the super-blocks of this step
-            const int nstep = nb - sb0 < 8 ? nb - sb0 : 8;
             float s_acc = acc[r];
             for (int gg = 0; gg < nstep; gg++) s_acc = s_acc + readlane_f(term, gg * 8);
             acc[r] = s_acc;
         }
+        if (more) cur = nxt;
     }
     if (lane == 0) {
+#pragma unroll
         for (int r = 0; r < R; r++)
             if (rvalid[r]) store_row(a, grow0 + r, tok, acc[r]);
+    }
+}
+
+// Rows of at most 64 super-blocks: lane = (row slot rs, super-block s),
+// RL row slots of nb lanes per wave. A lane holds the activation of its
+// super-block in registers for all its rows, loads its super-block's
+// chunks (each chunk index is one contiguous run over the row, see the
+// chunk-major layout), and computes the exact integer sums and the f32 term
+// d*sumi - dmin*summ alone. The row's terms are then folded in super-block
+// order by one lane through LDS. A wave does G row groups, the next group's
+// weights in flight while the current one is computed.
+template <int KIND>
+struct KqGeom {
+    static constexpr int CH = KIND == AOTK_Q4_K ? 9 : (KIND == AOTK_Q5_K ? 11 : 13);  // 16-byte chunks
+    static constexpr int RB = KIND == AOTK_Q4_K ? 144 : (KIND == AOTK_Q5_K ? 176 : 208);  // plane-0 bytes
+};
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int KIND>
+__device__ __forceinline__ float kq_term(const uint4 (&c)[KqGeom<KIND>::CH], float d6, const uint32_t (&y)[64],
+                                         const int (&bs)[16], float yd) {
+    int sumi = 0;
+    if (KIND == AOTK_Q4_K || KIND == AOTK_Q5_K) {
+        constexpr int QC = KIND == AOTK_Q4_K ? 1 : 3;
+        const uint4 hdr = c[0];
+        int summ = 0;
+        uint32_t hq[8];
+        if (KIND == AOTK_Q5_K) {
+            hq[0] = c[1].x; hq[1] = c[1].y; hq[2] = c[1].z; hq[3] = c[1].w;
+            hq[4] = c[2].x; hq[5] = c[2].y; hq[6] = c[2].z; hq[7] = c[2].w;
+        }
+#pragma unroll
+        for (int jp = 0; jp < 4; jp++) {
+            const uint4 q0 = c[QC + 2 * jp], q1 = c[QC + 2 * jp + 1];
+            const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            int slo = 0, shi = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                uint32_t lo = qw[k] & 0x0F0F0F0Fu;
+                uint32_t hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
+                if (KIND == AOTK_Q5_K) {
+                    lo |= ((hq[k] >> (2 * jp)) & 0x01010101u) << 4;
+                    hi |= ((hq[k] >> (2 * jp + 1)) & 0x01010101u) << 4;
+                }
+                slo = dot4(lo, y[16 * jp + k], slo);
+                shi = dot4(hi, y[16 * jp + 8 + k], shi);
+            }
+            int sc0, m0, sc1, m1;
+            scale_min_k4(2 * jp, hdr.y, hdr.z, hdr.w, sc0, m0);
+            scale_min_k4(2 * jp + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
+            sumi += sc0 * slo + sc1 * shi;
+            summ += m0 * (bs[4 * jp] + bs[4 * jp + 1]) + m1 * (bs[4 * jp + 2] + bs[4 * jp + 3]);
+        }
+        const float dd = f16_to_f32(hdr.x & 0xFFFFu) * yd;
+        const float dm = f16_to_f32(hdr.x >> 16) * yd;
+        return dd * (float)sumi - dm * (float)summ;
+    } else {
+        const uint4 scv = c[12];
+        const uint32_t scw[4] = {scv.x, scv.y, scv.z, scv.w};
+#pragma unroll
+        for (int g = 0; g < 16; g++) {
+            const int n = g >> 3, quarter = (g & 7) >> 1, half = g & 1;
+            const uint4 l4 = c[4 * n + 2 * (quarter & 1) + half];
+            const uint4 h4 = c[8 + 2 * n + half];
+            const uint32_t lw[4] = {l4.x, l4.y, l4.z, l4.w};
+            const uint32_t hw[4] = {h4.x, h4.y, h4.z, h4.w};
+            int sg = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t nib = quarter >= 2 ? (lw[k] >> 4) & 0x0F0F0F0Fu : lw[k] & 0x0F0F0F0Fu;
+                const uint32_t v = nib | (((hw[k] >> (2 * quarter)) & 0x03030303u) << 4);
+                sg = dot4(v, y[4 * g + k], sg);
+            }
+            const int sc = (int)(int8_t)((scw[g >> 2] >> (8 * (g & 3))) & 0xFFu);
+            sumi += sc * (sg - 32 * bs[g]);
+        }
+        const float dd = d6 * yd;
+        return dd * (float)sumi;
+    }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void k_mv_kq(MvArgs a, int RL, int G) {
+    using Geo = KqGeom<KIND>;
+    constexpr int CH = Geo::CH;
+    __shared__ float sT[4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tok = blockIdx.y;
+    const int nb = a.nb;
+    const int rs = lane / nb, s = lane - rs * nb;
+    const bool lane_on = rs < RL;
+    const int sa = lane_on ? s : 0;
+    // activation of super-block s
+    uint32_t y[64];
+    int bs[16];
+    {
+        const uint4 *xq = (const uint4 *)(a.xq + (size_t)tok * a.cols + (size_t)sa * 256);
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const uint4 v = xq[k];
+            y[4 * k] = v.x;
+            y[4 * k + 1] = v.y;
+            y[4 * k + 2] = v.z;
+            y[4 * k + 3] = v.w;
+        }
+        const uint4 *bp = (const uint4 *)(a.xbs + ((size_t)tok * nb + sa) * 16);
+        const uint4 b0 = bp[0], b1 = bp[1];
+        const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            bs[2 * k] = (int)(int16_t)(bw[k] & 0xFFFFu);
+            bs[2 * k + 1] = (int)(int16_t)(bw[k] >> 16);
+        }
+    }
+    const float yd = a.xd[(size_t)tok * nb + sa];
+    const size_t cs = (size_t)nb * 16;
+    const size_t rowb = (size_t)nb * Geo::RB;
+    const int group0 = (blockIdx.x * 4 + wave) * G;
+
+    uint4 cur[CH], nxt[CH];
+    float dcur = 0.0f, dnxt = 0.0f;
+    auto load = [&](uint4 (&c)[CH], float &d6, int gi) {
+        const int row = (group0 + gi) * RL + rs;
+        const bool on = lane_on && row < a.total_rows;
+        int local;
+        const int sg = seg_of(a, on ? row : 0, local);
+        const uint8_t *wp = a.w[sg] + (size_t)local * rowb + (size_t)sa * 16;
+#pragma unroll
+        for (int k = 0; k < CH; k++) c[k] = on ? *(const uint4 *)(wp + k * cs) : make_uint4(0, 0, 0, 0);
+        if (KIND == AOTK_Q6_K) d6 = on ? f16_to_f32(((const uint16_t *)a.w1[sg])[(size_t)local * nb + sa]) : 0.0f;
+    };
+    load(cur, dcur, 0);
+    for (int gi = 0; gi < G; gi++) {
+        const int gr0 = (group0 + gi) * RL;
+        if (gr0 >= a.total_rows) break;
+        if (gi + 1 < G) load(nxt, dnxt, gi + 1);
+        const float term = kq_term<KIND>(cur, dcur, y, bs, yd);
+        sT[wave][lane] = term;
+        wave_lds_sync();
+        if (lane < RL && gr0 + lane < a.total_rows) {
+            const float *tp = &sT[wave][lane * nb];
+            float acc = 0.0f;
+            for (int k = 0; k < nb; k++) acc = acc + tp[k];
+            store_row(a, gr0 + lane, tok, acc);
+        }
+        wave_lds_sync();
+        if (gi + 1 < G) {
+#pragma unroll
+            for (int k = 0; k < CH; k++) cur[k] = nxt[k];
+            dcur = dnxt;
+        }
     }
 }
 
@@ -368,21 +559,34 @@ static MvArgs make_args(int n, const DevWeight *const ws[], float *const ys[], c
     return a;
 }
 
+template <int KIND>
+static void launch_kq(const MvArgs &a, dim3 grid, hipStream_t s) {
+    if (a.nb <= 64) {
+        int RL = 1;
+        while (RL * 2 * a.nb <= 64) RL *= 2;
+        const int groups = (a.total_rows + RL - 1) / RL;
+        int G = (groups + 2047) / 2048;
+        G = G < 1 ? 1 : (G > 8 ? 8 : G);
+        grid.x = (unsigned)((groups + 4 * G - 1) / (4 * G));
+        k_mv_kq<KIND><<<grid, 256, 0, s>>>(a, RL, G);
+    } else {
+        grid.x = (unsigned)((a.total_rows + 7) / 8);
+        k_mv_kquant<KIND, 2><<<grid, 256, 0, s>>>(a);
+    }
+}
+
 static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
     dim3 grid;
     grid.y = (unsigned)m;
     switch (kind) {
     case AOTK_Q4_K:
-        grid.x = (unsigned)((a.total_rows + 7) / 8);
-        k_mv_kquant<AOTK_Q4_K, 2><<<grid, 256, 0, s>>>(a);
+        launch_kq<AOTK_Q4_K>(a, grid, s);
         break;
     case AOTK_Q5_K:
-        grid.x = (unsigned)((a.total_rows + 7) / 8);
-        k_mv_kquant<AOTK_Q5_K, 2><<<grid, 256, 0, s>>>(a);
+        launch_kq<AOTK_Q5_K>(a, grid, s);
         break;
     case AOTK_Q6_K:
-        grid.x = (unsigned)((a.total_rows + 7) / 8);
-        k_mv_kquant<AOTK_Q6_K, 2><<<grid, 256, 0, s>>>(a);
+        launch_kq<AOTK_Q6_K>(a, grid, s);
         break;
     case AOTK_Q8_0:
         grid.x = (unsigned)((a.total_rows + 31) / 32);

@@ -12,6 +12,7 @@
 #include "device.hpp"
 #include "formats.hpp"
 #include "internal.hpp"
+#include "seqsum.hpp"
 
 namespace aotk {
 
@@ -37,20 +38,47 @@ __device__ float block_sum(float v, float *red) {
     return t;
 }
 
+// Sequential f32 sum of n LDS values in index order, by one thread. Reads are
+// issued 32 values ahead of the dependent add chain so the chain runs at
+// VALU latency. n % 4 == 0, v 16-byte aligned.
+template <bool SQUARE>
+__device__ __forceinline__ float seq_sum_lds(const float *v, int n) {
+    float s = 0.0f;
+    int i = 0;
+    float4 cur[8];
+    int nfull = n / 32 * 32;
+    if (nfull > 0)
+        for (int k = 0; k < 8; k++) cur[k] = *(const float4 *)(v + 4 * k);
+    for (; i < nfull; i += 32) {
+        float4 nxt[8];
+        const bool more = i + 32 < nfull;
+        if (more)
+            for (int k = 0; k < 8; k++) nxt[k] = *(const float4 *)(v + i + 32 + 4 * k);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            if (SQUARE) {
+                s += cur[k].x * cur[k].x;
+                s += cur[k].y * cur[k].y;
+                s += cur[k].z * cur[k].z;
+                s += cur[k].w * cur[k].w;
+            } else {
+                s += cur[k].x;
+                s += cur[k].y;
+                s += cur[k].z;
+                s += cur[k].w;
+            }
+        }
+        if (more)
+            for (int k = 0; k < 8; k++) cur[k] = nxt[k];
+    }
+    for (; i < n; i++) s += SQUARE ? v[i] * v[i] : v[i];
+    return s;
+}
+
 // ss = sum of v*v over n values in LDS, in index order (ops.rs:10-13). Run
 // by one thread; the result is broadcast through LDS.
 __device__ float seq_sumsq_lds(const float *v, int n, float *bcast) {
-    if (threadIdx.x == 0) {
-        float ss = 0.0f;
-        for (int i = 0; i < n; i += 4) {
-            float4 q = *(const float4 *)(v + i);
-            ss += q.x * q.x;
-            ss += q.y * q.y;
-            ss += q.z * q.z;
-            ss += q.w * q.w;
-        }
-        *bcast = ss;
-    }
+    if (threadIdx.x == 0) *bcast = seq_sum_lds<true>(v, n);
     __syncthreads();
     return *bcast;
 }
@@ -126,17 +154,22 @@ __device__ __forceinline__ ActQ8_0 q80_row(ActQ8_0 a, size_t row, size_t n) {
 
 // rmsnorm (ops.rs:7-18) of row blockIdx.x, then quantization of the result.
 // n % 256 == 0, n <= 8192 (the normalised row is staged in LDS).
-__global__ __launch_bounds__(1024) void k_rmsnorm_quant(const float *__restrict__ x, const float *__restrict__ w, int n,
+__global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant(const float *__restrict__ x, const float *__restrict__ w, int n,
                                                          float eps, RmsOut out) {
     __shared__ __align__(16) float row[8192];
-    __shared__ float bc;
+    __shared__ float sq[SEQ_PAD_N];
+    __shared__ SeqScratch S;
     const size_t m = blockIdx.x;
     const float *xr = x + m * n;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) row[i] = xr[i];
+    const int C = seq_chunk(n);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = xr[i];
+        row[i] = v;
+        sq[seq_idx(i, C)] = v * v;
+    }
     __syncthreads();
-    float ss = seq_sumsq_lds(row, n, &bc);
+    float ss = exact_seq_sum(sq, n, S);
     float r = 1.0f / sqrtf(ss / (float)n + eps);
-    __syncthreads();
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         float v = row[i] * r * w[i];
         row[i] = v;
@@ -154,7 +187,7 @@ __global__ __launch_bounds__(1024) void k_rmsnorm_quant(const float *__restrict_
 }
 
 void launch_rmsnorm_quant(const float *x, const float *w, size_t n, size_t m, float eps, RmsOut out, hipStream_t s) {
-    k_rmsnorm_quant<<<(unsigned)m, 1024, 0, s>>>(x, w, (int)n, eps, out);
+    k_rmsnorm_quant<<<(unsigned)m, SEQ_T, 0, s>>>(x, w, (int)n, eps, out);
 }
 
 // Quantize m rows of n floats (n % 256 == 0), one wave per 256 values.
@@ -315,82 +348,105 @@ __device__ __forceinline__ void row_range(const AttnArgs &a, size_t i, size_t &t
     t0 = (a.window > 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
 }
 
+// Scores: block = (kv head, chunk of ATT_CH positions, row), gqa * 64
+// threads. The chunk's K rows are staged in LDS (coalesced row loads, row
+// stride HD + 1 so that lanes reading one dimension of 64 rows hit 64
+// banks); thread (query head of the group, position) then runs its dot
+// product sequentially over the head dimension.
 template <int HD>
-__global__ __launch_bounds__(64) void k_attn_scores(AttnArgs a) {
-    __shared__ float sq[ATT_MAX_GQA][HD];
-    const int lane = threadIdx.x;
+__global__ __launch_bounds__(512) void k_attn_scores(AttnArgs a) {
+    constexpr int KS = HD + 1;
+    __shared__ float sk[ATT_CH * KS];
+    __shared__ __align__(16) float sq[ATT_MAX_GQA][HD];
+    const int gqa = a.n_head / a.n_kv_head;
+    const int lane = threadIdx.x & 63, hg = threadIdx.x >> 6;
     const int kvh = blockIdx.x, c = blockIdx.y;
     const size_t i = blockIdx.z;
-    const int gqa = a.n_head / a.n_kv_head;
     size_t t0, n;
     row_range(a, i, t0, n);
     const size_t start = t0 + (size_t)c * ATT_CH;
     if (start >= n) return;
+    const int rows = (int)min((size_t)ATT_CH, n - start);
     const size_t kv = (size_t)a.n_kv_head * HD, q_dim = (size_t)a.n_head * HD;
-    for (int h = 0; h < gqa; h++)
-        for (int e = lane; e < HD; e += 64) sq[h][e] = a.q[i * q_dim + (size_t)(kvh * gqa + h) * HD + e];
-    __syncthreads();
-    const size_t t = start + lane;
-    if (t >= n) return;
-    const float4 *kr = (const float4 *)(a.k_cache + t * kv + (size_t)kvh * HD);
-    float acc[ATT_MAX_GQA];
-    for (int h = 0; h < gqa; h++) acc[h] = 0.0f;
-    for (int d4 = 0; d4 < HD / 4; d4++) {
-        float4 k4 = kr[d4];
-        for (int h = 0; h < gqa; h++) {
-            const float *qq = &sq[h][4 * d4];
-            float s = acc[h];
-            s += qq[0] * k4.x;
-            s += qq[1] * k4.y;
-            s += qq[2] * k4.z;
-            s += qq[3] * k4.w;
-            acc[h] = s;
-        }
+    for (int e = lane; e < HD; e += 64) sq[hg][e] = a.q[i * q_dim + (size_t)(kvh * gqa + hg) * HD + e];
+    const float *kb = a.k_cache + start * kv + (size_t)kvh * HD;
+    constexpr int R4 = HD / 4;
+    for (int idx = threadIdx.x; idx < rows * R4; idx += blockDim.x) {
+        const int r = idx / R4, c4 = idx % R4;
+        const float4 k4 = *(const float4 *)(kb + (size_t)r * kv + 4 * c4);
+        float *d = sk + r * KS + 4 * c4;
+        d[0] = k4.x;
+        d[1] = k4.y;
+        d[2] = k4.z;
+        d[3] = k4.w;
     }
-    for (int h = 0; h < gqa; h++)
-        a.prob[(i * a.n_head + (size_t)(kvh * gqa + h)) * a.span + (t - t0)] = acc[h] * a.scale;
+    __syncthreads();
+    if (lane >= rows) return;
+    const float *kr = sk + lane * KS;
+    const float *qq = sq[hg];
+    float s = 0.0f;
+#pragma unroll 16
+    for (int d = 0; d < HD; d++) s += qq[d] * kr[d];
+    a.prob[(i * a.n_head + (size_t)(kvh * gqa + hg)) * a.span + (start + lane - t0)] = s * a.scale;
 }
 
-__global__ __launch_bounds__(256) void k_attn_softmax(AttnArgs a) {
-    __shared__ float red[4];
+// Softmax per (row, head), staged in LDS (span <= ATT_MAX_SPAN).
+constexpr int ATT_MAX_SPAN = 16384;
+__global__ __launch_bounds__(SEQ_T) void k_attn_softmax(AttnArgs a) {
+    __shared__ __align__(16) float e[ATT_MAX_SPAN + 64];
+    __shared__ SeqScratch S;
+    __shared__ float red[SEQ_T / 64];
     __shared__ float bc;
     const int h = blockIdx.x;
     const size_t i = blockIdx.y;
     size_t t0, n;
     row_range(a, i, t0, n);
     const int cnt = (int)(n - t0);
+    // scores in the padded chunk layout of the exact sum when it applies
+    const bool exact = cnt <= SEQ_MAX_N;
+    const int C = seq_chunk(cnt);
+    auto at = [&](int t) { return exact ? seq_idx(t, C) : t; };
     float *p = a.prob + (i * a.n_head + h) * a.span;
     float mx = -INFINITY;
-    for (int t = threadIdx.x; t < cnt; t += blockDim.x) mx = fmaxf(mx, p[t]);
+    for (int t = threadIdx.x; t < cnt; t += blockDim.x) {
+        float v = p[t];
+        e[at(t)] = v;
+        mx = fmaxf(mx, v);
+    }
     mx = wave_max(mx);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int t = threadIdx.x; t < cnt; t += blockDim.x) p[t] = aotk_expf(p[t] - mx);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float sum = 0.0f;
-        int t = 0;
-        for (; t + 4 <= cnt; t += 4) {
-            float4 e = *(const float4 *)(p + t);
-            sum += e.x;
-            sum += e.y;
-            sum += e.z;
-            sum += e.w;
-        }
-        for (; t < cnt; t++) sum += p[t];
-        bc = 1.0f / sum;
+    {
+        const int lane = threadIdx.x & 63;
+        mx = wave_max(lane < SEQ_T / 64 ? red[lane] : -INFINITY);
     }
+    for (int t = threadIdx.x; t < cnt; t += blockDim.x) e[at(t)] = aotk_expf(e[at(t)] - mx);
     __syncthreads();
-    const float inv = bc;
-    for (int t = threadIdx.x; t < cnt; t += blockDim.x) p[t] = p[t] * inv;
+    float sum;
+    if (exact) {
+        sum = exact_seq_sum(e, cnt, S);
+    } else {
+        if (threadIdx.x == 0) bc = seq_sum_lds<false>(e, cnt);
+        __syncthreads();
+        sum = bc;
+    }
+    const float inv = 1.0f / sum;
+    for (int t = threadIdx.x; t < cnt; t += blockDim.x) p[t] = e[at(t)] * inv;
 }
 
-// Block = 64 output dims of one head of one row.
+// Output: block = one wave, AO_DB dims of one head. Products p_t * v_t,d
+// of a chunk of AO_TC positions are formed by the whole wave (float4 V
+// loads, 16 positions per pass) into LDS; lanes 0..AO_DB-1 then add them in
+// position order. The next chunk's loads are in flight during the adds.
+constexpr int AO_DB = 16;
+constexpr int AO_TC = 256;
 __global__ __launch_bounds__(64) void k_attn_out(AttnArgs a) {
+    __shared__ __align__(16) float buf[2][AO_TC * AO_DB];
+    constexpr int NP = AO_TC / 16;
+    const int lane = threadIdx.x;
     const int hd = a.hd;
-    const int per_head = hd / 64;
-    const int h = blockIdx.x / per_head, d = (blockIdx.x % per_head) * 64 + threadIdx.x;
+    const int per_head = hd / AO_DB;
+    const int h = blockIdx.x / per_head, d0 = (blockIdx.x % per_head) * AO_DB;
     const size_t i = blockIdx.y;
     const int gqa = a.n_head / a.n_kv_head;
     const int kvh = h / gqa;
@@ -399,21 +455,51 @@ __global__ __launch_bounds__(64) void k_attn_out(AttnArgs a) {
     const int cnt = (int)(n - t0);
     const size_t kv = (size_t)a.n_kv_head * hd;
     const float *p = a.prob + (i * a.n_head + h) * a.span;
-    const float *vp = a.v_cache + t0 * kv + (size_t)kvh * hd + d;
-    float o = 0.0f;
-    int t = 0;
-    for (; t + 8 <= cnt; t += 8) {
-        float v[8], w[8];
+    const float *vb = a.v_cache + t0 * kv + (size_t)kvh * hd + d0 + 4 * (lane & 3);
+    const int r = lane >> 2;
+    float4 R[NP];
+    float Pp[NP];
+    auto issue = [&](int base) {
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            v[k] = vp[(size_t)(t + k) * kv];
-            w[k] = p[t + k];
+        for (int j = 0; j < NP; j++) {
+            const int t = base + r + 16 * j;
+            if (t < cnt) {
+                R[j] = *(const float4 *)(vb + (size_t)t * kv);
+                Pp[j] = p[t];
+            } else {
+                R[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                Pp[j] = 0.0f;
+            }
         }
+    };
+    const int nch = (cnt + AO_TC - 1) / AO_TC;
+    float o = 0.0f;
+    issue(0);
+    for (int c = 0; c < nch; c++) {
+        float *b = buf[c & 1];
 #pragma unroll
-        for (int k = 0; k < 8; k++) o += w[k] * v[k];
+        for (int j = 0; j < NP; j++) {
+            const float pj = Pp[j];
+            *(float4 *)(b + (r + 16 * j) * AO_DB + 4 * (lane & 3)) =
+                make_float4(pj * R[j].x, pj * R[j].y, pj * R[j].z, pj * R[j].w);
+        }
+        __syncthreads();
+        if (c + 1 < nch) issue((c + 1) * AO_TC);
+        const int len = min(AO_TC, cnt - c * AO_TC);
+        if (lane < AO_DB) {
+            const float *bp = b + lane;
+            int t = 0;
+            for (; t + 16 <= len; t += 16) {
+                float v[16];
+#pragma unroll
+                for (int k = 0; k < 16; k++) v[k] = bp[(t + k) * AO_DB];
+#pragma unroll
+                for (int k = 0; k < 16; k++) o += v[k];
+            }
+            for (; t < len; t++) o += bp[t * AO_DB];
+        }
     }
-    for (; t < cnt; t++) o += p[t] * vp[(size_t)t * kv];
-    a.out[i * (size_t)a.n_head * hd + (size_t)h * hd + d] = o;
+    if (lane < AO_DB) a.out[i * (size_t)a.n_head * hd + (size_t)h * hd + d0 + lane] = o;
 }
 
 size_t attention_scratch_bytes(size_t n_head, size_t head_dim, size_t ctx, size_t m) {
@@ -441,13 +527,14 @@ void launch_attention(float *out, const float *q, const float *k_cache, const fl
     a.scale = 1.0f / sqrtf((float)head_dim);
     size_t span = window > 0 && window < ctx_rows ? window : ctx_rows;
     dim3 grid((unsigned)n_kv_head, (unsigned)((span + ATT_CH - 1) / ATT_CH), (unsigned)m);
+    const unsigned threads = (unsigned)(64 * (n_head / n_kv_head));
     switch (head_dim) {
-    case 64: k_attn_scores<64><<<grid, 64, 0, s>>>(a); break;
-    case 128: k_attn_scores<128><<<grid, 64, 0, s>>>(a); break;
-    default: k_attn_scores<256><<<grid, 64, 0, s>>>(a); break;
+    case 64: k_attn_scores<64><<<grid, threads, 0, s>>>(a); break;
+    case 128: k_attn_scores<128><<<grid, threads, 0, s>>>(a); break;
+    default: k_attn_scores<256><<<grid, threads, 0, s>>>(a); break;
     }
-    k_attn_softmax<<<dim3((unsigned)n_head, (unsigned)m), 256, 0, s>>>(a);
-    k_attn_out<<<dim3((unsigned)(n_head * head_dim / 64), (unsigned)m), 64, 0, s>>>(a);
+    k_attn_softmax<<<dim3((unsigned)n_head, (unsigned)m), SEQ_T, 0, s>>>(a);
+    k_attn_out<<<dim3((unsigned)(n_head * head_dim / AO_DB), (unsigned)m), 64, 0, s>>>(a);
 }
 
 // ------------------------------------------------------------ elementwise
@@ -461,20 +548,26 @@ void launch_add(float *x, const float *y, size_t n, hipStream_t s) {
 }
 
 // Gemma post-norm join: x += rmsnorm(y) (emit.rs:320-324).
-__global__ __launch_bounds__(1024) void k_rmsnorm_add(float *x, const float *y, const float *w, int n, float eps) {
+__global__ __launch_bounds__(SEQ_T) void k_rmsnorm_add(float *x, const float *y, const float *w, int n, float eps) {
     __shared__ __align__(16) float row[8192];
-    __shared__ float bc;
+    __shared__ float sq[SEQ_PAD_N];
+    __shared__ SeqScratch S;
     const size_t m = blockIdx.x;
     const float *yr = y + m * n;
     float *xr = x + m * n;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) row[i] = yr[i];
+    const int C = seq_chunk(n);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = yr[i];
+        row[i] = v;
+        sq[seq_idx(i, C)] = v * v;
+    }
     __syncthreads();
-    float ss = seq_sumsq_lds(row, n, &bc);
+    float ss = exact_seq_sum(sq, n, S);
     float r = 1.0f / sqrtf(ss / (float)n + eps);
     for (int i = threadIdx.x; i < n; i += blockDim.x) xr[i] = xr[i] + row[i] * r * w[i];
 }
 void launch_rmsnorm_add(float *x, const float *y, const float *w, size_t n, size_t m, float eps, hipStream_t s) {
-    k_rmsnorm_add<<<(unsigned)m, 1024, 0, s>>>(x, y, w, (int)n, eps);
+    k_rmsnorm_add<<<(unsigned)m, SEQ_T, 0, s>>>(x, y, w, (int)n, eps);
 }
 
 __global__ void k_silu_mul(float *h, const float *up, size_t n, int gelu) {
@@ -487,9 +580,11 @@ void launch_silu_mul(float *h, const float *up, size_t n, int gelu, hipStream_t 
 }
 
 // softmax (ops.rs:98-112) of one vector: max, exp, sequential sum, scale.
-__global__ __launch_bounds__(1024) void k_softmax(float *x, int n) {
+__global__ __launch_bounds__(SEQ_T) void k_softmax(float *x, int n) {
     __shared__ float red[16];
     __shared__ float bc;
+    __shared__ float ev[SEQ_PAD_N];
+    __shared__ SeqScratch S;
     float mx = -INFINITY;
     for (int i = threadIdx.x; i < n; i += blockDim.x) mx = fmaxf(mx, x[i]);
     mx = wave_max(mx);
@@ -499,16 +594,25 @@ __global__ __launch_bounds__(1024) void k_softmax(float *x, int n) {
     mx = wave_max(t);
     for (int i = threadIdx.x; i < n; i += blockDim.x) x[i] = aotk_expf(x[i] - mx);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float sum = 0.0f;
-        for (int i = 0; i < n; i++) sum += x[i];
-        bc = 1.0f / sum;
+    float sum;
+    if (n <= SEQ_MAX_N) {
+        const int C = seq_chunk(n);
+        for (int i = threadIdx.x; i < n; i += blockDim.x) ev[seq_idx(i, C)] = x[i];
+        __syncthreads();
+        sum = exact_seq_sum(ev, n, S);
+    } else {
+        if (threadIdx.x == 0) {
+            float t = 0.0f;
+            for (int i = 0; i < n; i++) t += x[i];
+            bc = t;
+        }
+        __syncthreads();
+        sum = bc;
     }
-    __syncthreads();
-    float inv = bc;
+    float inv = 1.0f / sum;
     for (int i = threadIdx.x; i < n; i += blockDim.x) x[i] = x[i] * inv;
 }
-void launch_softmax(float *x, size_t n, hipStream_t s) { k_softmax<<<1, 1024, 0, s>>>(x, (int)n); }
+void launch_softmax(float *x, size_t n, hipStream_t s) { k_softmax<<<1, SEQ_T, 0, s>>>(x, (int)n); }
 
 void launch_rmsnorm_heads(float *x, const float *w, size_t n_heads, size_t head_dim, float eps, hipStream_t s) {
     QkvPost p = {};

@@ -42,33 +42,43 @@ void weight_set_planes(DevWeight &w, uint8_t *base) {
 }
 
 // Planar formats: how a reference block of TS bytes maps onto the planes.
-// Q6_K: [0,208) -> p0 (208/blk), [208,210) -> p1 (2/blk)
+// Q4_K / Q5_K: chunk-major row in p0
+// Q6_K: [0,208) -> chunk-major row in p0, [208,210) -> p1 (2/blk)
 // Q8_0: [0,2) -> p1, [2,34) -> p0 (32/blk)
 // Q4_0: [0,2) -> p1, [2,18) -> p0 (16/blk)
 // Q5_0: [0,2) -> p1, [2,6) -> p2 (4/blk), [6,22) -> p0 (16/blk)
 template <int KIND>
 struct Planar;
+template <> struct Planar<AOTK_Q4_K> { static constexpr int TS = 144; };
+template <> struct Planar<AOTK_Q5_K> { static constexpr int TS = 176; };
 template <> struct Planar<AOTK_Q6_K> { static constexpr int TS = 210; };
 template <> struct Planar<AOTK_Q8_0> { static constexpr int TS = 34; };
 template <> struct Planar<AOTK_Q4_0> { static constexpr int TS = 18; };
 template <> struct Planar<AOTK_Q5_0> { static constexpr int TS = 22; };
 
 template <int KIND>
-__device__ __forceinline__ uint8_t *plane_byte(size_t blk, int off, uint8_t *p0, uint8_t *p1, uint8_t *p2) {
-    if (KIND == AOTK_Q6_K) return off < 208 ? p0 + blk * 208 + off : p1 + blk * 2 + (off - 208);
+__device__ __forceinline__ uint8_t *plane_byte(size_t blk, size_t nb, int off, uint8_t *p0, uint8_t *p1, uint8_t *p2) {
+    if (KIND == AOTK_Q4_K || KIND == AOTK_Q5_K) {
+        const size_t r = blk / nb, sb = blk % nb;
+        return p0 + r * nb * Planar<KIND>::TS + kq_off(off, sb, nb);
+    }
+    if (KIND == AOTK_Q6_K) {
+        const size_t r = blk / nb, sb = blk % nb;
+        return off < 208 ? p0 + r * nb * 208 + kq_off(off, sb, nb) : p1 + blk * 2 + (off - 208);
+    }
     if (KIND == AOTK_Q8_0) return off < 2 ? p1 + blk * 2 + off : p0 + blk * 32 + (off - 2);
     if (KIND == AOTK_Q4_0) return off < 2 ? p1 + blk * 2 + off : p0 + blk * 16 + (off - 2);
     return off < 2 ? p1 + blk * 2 + off : (off < 6 ? p2 + blk * 4 + (off - 2) : p0 + blk * 16 + (off - 6));
 }
 
 template <int KIND, bool TO_PLANES>
-__global__ void k_repack(size_t nblk, uint8_t *raw, uint8_t *p0, uint8_t *p1, uint8_t *p2) {
+__global__ void k_repack(size_t nblk, size_t nb, uint8_t *raw, uint8_t *p0, uint8_t *p1, uint8_t *p2) {
     size_t blk = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (blk >= nblk) return;
     constexpr int TS = Planar<KIND>::TS;
     uint8_t *src = raw + blk * TS;  // rows are contiguous: block index is global
     for (int off = 0; off < TS; off++) {
-        uint8_t *pb = plane_byte<KIND>(blk, off, p0, p1, p2);
+        uint8_t *pb = plane_byte<KIND>(blk, nb, off, p0, p1, p2);
         if (TO_PLANES) *pb = src[off];
         else src[off] = *pb;
     }
@@ -80,10 +90,15 @@ static void repack_common(const DevWeight &w, uint8_t *raw, hipStream_t s) {
     size_t bytes = w.rows * row_bytes(w.kind, w.cols);
     unsigned grid = (unsigned)((nblk + 255) / 256);
     switch (w.kind) {
-    case AOTK_Q6_K: k_repack<AOTK_Q6_K, TO_PLANES><<<grid, 256, 0, s>>>(nblk, raw, w.plane[0], w.plane[1], w.plane[2]); break;
-    case AOTK_Q8_0: k_repack<AOTK_Q8_0, TO_PLANES><<<grid, 256, 0, s>>>(nblk, raw, w.plane[0], w.plane[1], w.plane[2]); break;
-    case AOTK_Q4_0: k_repack<AOTK_Q4_0, TO_PLANES><<<grid, 256, 0, s>>>(nblk, raw, w.plane[0], w.plane[1], w.plane[2]); break;
-    case AOTK_Q5_0: k_repack<AOTK_Q5_0, TO_PLANES><<<grid, 256, 0, s>>>(nblk, raw, w.plane[0], w.plane[1], w.plane[2]); break;
+#define AOTK_REPACK(K) \
+    case K: k_repack<K, TO_PLANES><<<grid, 256, 0, s>>>(nblk, w.nb, raw, w.plane[0], w.plane[1], w.plane[2]); break;
+        AOTK_REPACK(AOTK_Q4_K)
+        AOTK_REPACK(AOTK_Q5_K)
+        AOTK_REPACK(AOTK_Q6_K)
+        AOTK_REPACK(AOTK_Q8_0)
+        AOTK_REPACK(AOTK_Q4_0)
+        AOTK_REPACK(AOTK_Q5_0)
+#undef AOTK_REPACK
     default:
         if (TO_PLANES) (void)hipMemcpyAsync(w.plane[0], raw, bytes, hipMemcpyDeviceToDevice, s);
         else (void)hipMemcpyAsync(raw, w.plane[0], bytes, hipMemcpyDeviceToDevice, s);

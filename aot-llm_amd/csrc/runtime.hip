@@ -367,6 +367,7 @@ int aotk_attention(float *out_dev, const float *q_dev, const float *k_cache_dev,
     if (head_dim != 64 && head_dim != 128 && head_dim != 256) return fail("attention: head_dim %zu unsupported", head_dim);
     if (n_kv_head == 0 || n_head % n_kv_head || n_head / n_kv_head > 8) return fail("attention: bad head counts");
     if (pos0 + m > ctx) return fail("attention: positions exceed the context");
+    if (ctx > 16384) return fail("attention: context %zu exceeds 16384 positions", ctx);
     size_t kv = n_kv_head * head_dim;
     size_t bytes = attention_scratch_bytes(n_head, head_dim, ctx, m);
     void *s = scratch(bytes);
@@ -768,8 +769,8 @@ aotk_state *aotk_state_new(aotk_model *m, size_t ctx, size_t max_batch) {
         fail("null model");
         return nullptr;
     }
-    if (ctx == 0) {
-        fail("context must be positive");
+    if (ctx == 0 || ctx > 16384) {
+        fail("context %zu must be in 1..16384", ctx);
         return nullptr;
     }
     if (max_batch < 1) max_batch = 1;
@@ -1051,6 +1052,50 @@ int aotk_kv_upload(aotk_state *st, size_t n_pos, const float *k_host, const floa
         HIPC(hipMemcpyAsync(st->v_cache + l * st->ctx * kv, v_host + l * n_pos * kv, n_pos * kv * 4, hipMemcpyHostToDevice, g_stream));
     }
     HIPC(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int aotk_time_matvec(const aotk_weight *const *ws, size_t n_w, const float *x_dev, size_t iters, float *ms_per_launch) {
+    if (ensure_init()) return -1;
+    if (!ws || n_w == 0 || iters == 0) return fail("time_matvec: nothing to time");
+    const DevWeight &w0 = ws[0]->dw;
+    for (size_t i = 1; i < n_w; i++)
+        if (ws[i]->dw.kind != w0.kind || ws[i]->dw.cols != w0.cols || ws[i]->dw.rows != w0.rows)
+            return fail("time_matvec: weights differ in kind or shape");
+    int a = activation(w0.kind);
+    size_t act_bytes = a == ACT_Q8_K ? act_q8k_bytes(w0.cols, 1) : (a == ACT_Q8_0 ? act_q8_0_bytes(w0.cols, 1) : 0);
+    void *s = scratch(act_bytes + align_up(w0.rows * 4, 256));
+    if (!s) return -1;
+    float *y = (float *)((uint8_t *)s + act_bytes);
+    ActQ8K qk;
+    ActQ8_0 q0;
+    const void *act = x_dev;
+    if (a == ACT_Q8_K) {
+        qk = act_q8k_view(s, w0.cols, 1);
+        launch_quant_q8k(x_dev, w0.cols, 1, qk, g_stream);
+        act = &qk;
+    } else if (a == ACT_Q8_0) {
+        q0 = act_q8_0_view(s, w0.cols, 1);
+        launch_quant_q8_0(x_dev, w0.cols, 1, q0, g_stream);
+        act = &q0;
+    }
+    hipEvent_t e0, e1;
+    HIPC(hipEventCreate(&e0));
+    HIPC(hipEventCreate(&e1));
+    HIPC(hipEventRecord(e0, g_stream));
+    for (size_t it = 0; it < iters; it++) launch_matvec(ws[it % n_w]->dw, act, 1, y, nullptr, g_stream);
+    HIPC(hipEventRecord(e1, g_stream));
+    HIPC(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    HIPC(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    HIPC(hipGetLastError());
+    *ms_per_launch = ms / (float)iters;
     return 0;
 }
 

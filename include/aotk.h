@@ -259,6 +259,13 @@ int aotk_generate_greedy(aotk_state *state, size_t pos, size_t n, uint32_t *toke
  * reference's cache: [n_layer][n_pos][kv_dim] f32 for K, then the same for V. */
 int aotk_kv_download(aotk_state *state, size_t n_pos, float *k_host, float *v_host);
 int aotk_kv_upload(aotk_state *state, size_t n_pos, const float *k_host, const float *v_host);
+/* Measurement helper (the reference's #[ignore] bench_ops harness,
+ * crates/aot-kernels/tests/metal.rs:459-641): quantizes x_dev once, then
+ * launches the matvec of ws[0], ws[1], ... in turn (rotating copies keeps
+ * the working set out of the 256 MB Infinity Cache) `iters` times on the
+ * library stream, timed with HIP events; writes the mean ms per launch. */
+int aotk_time_matvec(const aotk_weight *const *ws, size_t n_w, const float *x_dev, size_t iters, float *ms_per_launch);
+
 /* The library's HIP stream (hipStream_t) for callers that time on it. */
 void *aotk_stream(void);
 

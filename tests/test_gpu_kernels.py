@@ -163,3 +163,45 @@ def test_libm_matched_exp_tanh(aotk, oracle):
         getattr(oracle.load(), name)(oracle.ptr(ref), oracle.ptr(up), ref.size)
         got = fn(h, up)
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), name
+
+
+def _stress_rows(rng, n):
+    rows = [rng.standard_normal(n), rng.standard_normal(n) * 1e-3, rng.standard_normal(n) * 50]
+    t = np.where(rng.random(n) < 0.3, 2.0 ** -12, 1.0)  # squares 2^-24 next to 1.0: exact ties
+    rows.append(t * rng.choice([1, -1], n))
+    t = rng.integers(0, 4, n).astype(np.float64)
+    t[: n // 8] = 0.0  # leading zeros
+    rows.append(t)
+    t = rng.standard_normal(n) * 1e-6
+    t[n // 2] = 1e3  # a huge element mid-way
+    rows.append(t)
+    t = rng.standard_normal(n) * 1e3
+    t[1:] *= 1e-9  # huge first element, then tiny ones
+    rows.append(t)
+    t = np.exp(rng.uniform(-20, 5, n)) * rng.choice([1, -1], n)  # wide dynamic range
+    rows.append(t)
+    rows.append(np.full(n, 3.0 * 2.0 ** -12))
+    return np.array(rows, np.float32)
+
+
+@pytest.mark.parametrize("n", [256, 2048, 2560, 4096, 8192])
+def test_exact_sequential_sum_rmsnorm(aotk, oracle, n):
+    """rmsnorm's sum of squares replays the reference's sequential order bit for bit."""
+    rng = np.random.default_rng(n)
+    x = _stress_rows(rng, n)
+    w = np.ones(n, np.float32)
+    got = aotk.rmsnorm(x, w, 1e-5)
+    ref = np.stack([_or_rmsnorm(oracle, r, w) for r in x])
+    bad = [i for i in range(len(x)) if not np.array_equal(got[i].view(np.uint32), ref[i].view(np.uint32))]
+    assert not bad, f"rows {bad} differ"
+
+
+@pytest.mark.parametrize("n", [7, 64, 1000, 4096, 8192, 9000])
+def test_exact_sequential_sum_softmax(aotk, oracle, n):
+    rng = np.random.default_rng(n + 1)
+    for s in (rng.standard_normal(n) * 4, rng.standard_normal(n) * 0.01, np.linspace(-30, 0, n),
+              np.where(rng.random(n) < 0.5, 0.0, -16.635532)):
+        s = s.astype(np.float32)
+        ref = s.copy()
+        oracle.load().or_softmax(oracle.ptr(ref), ref.size)
+        assert np.array_equal(aotk.softmax(s).view(np.uint32), ref.view(np.uint32))
