@@ -109,6 +109,7 @@ def load(path=None):
     _sig(lib, "aotk_h2d", i, [vp, vp, sz])
     _sig(lib, "aotk_d2h", i, [vp, vp, sz])
     _sig(lib, "aotk_memset", i, [vp, i, sz])
+    _sig(lib, "aotk_d2d", i, [vp, vp, sz])
     _sig(lib, "aotk_sync", i, [])
     _sig(lib, "aotk_row_bytes", sz, [i, sz])
     _sig(lib, "aotk_weight_upload", vp, [i, vp, sz, sz])

@@ -29,6 +29,12 @@ def _np_ptr(a):
     return a.ctypes.data_as(C.c_void_p)
 
 
+def copy_dev(dst, src, nbytes):
+    """Device-to-device copy of `nbytes` between DeviceBuffers (synchronous)."""
+    assert nbytes <= dst.nbytes and nbytes <= src.nbytes
+    abi.check(_lib().aotk_d2d(dst.ptr, src.ptr, nbytes))
+
+
 class DeviceBuffer:
     """A device allocation owned by Python."""
 

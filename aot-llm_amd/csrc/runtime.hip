@@ -117,6 +117,13 @@ int aotk_d2h(void *dst, const void *src, size_t bytes) {
     return 0;
 }
 
+int aotk_d2d(void *dst, const void *src, size_t bytes) {
+    if (ensure_init()) return -1;
+    HIPC(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_stream));
+    HIPC(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
 int aotk_memset(void *dst, int value, size_t bytes) {
     if (ensure_init()) return -1;
     HIPC(hipMemsetAsync(dst, value, bytes, g_stream));

@@ -72,6 +72,19 @@ def time_kernel(aotk, kind, rows, cols, iters=200, min_bytes=1 << 30):
     return ms, copies
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (FETCH_SIZE / WRITE_SIZE scaled by a copy kernel of known size),
+    or None when no summary for that kernel exists."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return t.get("traffic_bytes") if t.get("kernel") == kernel else None
+
+
 def cpu_baseline(spec, blob, n_prompt, budget_s):
     """Oracle forward on host cores: a short prompt, then decode until the
     time budget is spent; tok/s like the reference's stats line."""
@@ -102,6 +115,20 @@ def cpu_baseline(spec, blob, n_prompt, budget_s):
                 host_cpu=cpu_model(), host_cores=os.cpu_count(), prompt_tok_s=round(n_prompt / tp, 3))
 
 
+def micro_only():
+    """Short program for counter runs: 200 launches of the Q4_K 14336x4096
+    matvec over rotated copies, then one device-to-device copy of 256 MiB
+    (the calibration kernel: it reads and writes exactly 256 MiB)."""
+    import aotk
+    from aotk import abi
+    ms, copies = time_kernel(aotk, abi.Q4_K, 14336, 4096)
+    n = 256 << 20
+    src, dst = aotk.DeviceBuffer(n), aotk.DeviceBuffer(n)
+    aotk.copy_dev(dst, src, n)
+    aotk.sync()
+    log(f"q4_K 14336x4096: {ms * 1e3:.2f} us over {copies} copies; copied {n} bytes")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -113,6 +140,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-micro", action="store_true")
+    ap.add_argument("--micro-only", action="store_true",
+                    help="only the Q4_K 14336x4096 matvec and a 256 MiB device copy (for rocprofv3 --pmc runs)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one MI355X; the hot path has no multi-GPU mode "
@@ -122,6 +151,9 @@ def main():
     import aotk
     from aotk import abi, configs
     aotk.init(0)
+    if a.micro_only:
+        micro_only()
+        return
 
     spec = configs.build(a.config)
     spec.cfg["name"] = a.config
@@ -165,9 +197,10 @@ def main():
                                           copies=copies)
             log(f"q4_K matvec {rows}x{cols}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
         dom = micro["14336x4096"]
-        roofline = dict(bound="hbm", achieved=dom["GBs"], peak=HBM_PEAK_GBS, unit="GB/s", frac=dom["frac"], traffic=None,
-                        kernel="k_mv_kquant<Q4_K> 14336x4096 (ffn gate/up)",
-                        bytes_per_launch=matvec_bytes(abi.Q4_K, 14336, 4096))
+        roofline = dict(bound="hbm", achieved=dom["GBs"], peak=HBM_PEAK_GBS, unit="GB/s", frac=dom["frac"],
+                        traffic=measured_traffic("k_mv_kq<Q4_K> 14336x4096"),
+                        kernel="k_mv_kq<Q4_K> 14336x4096 (ffn gate/up shape)",
+                        bytes_per_launch=matvec_bytes(abi.Q4_K, 14336, 4096), us_per_launch=dom["us"])
 
     cpu = None
     if not a.no_cpu:

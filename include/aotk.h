@@ -127,6 +127,10 @@ int aotk_dev_free(void *ptr_dev);
 int aotk_h2d(void *dst_dev, const void *src_host, size_t bytes);
 int aotk_d2h(void *dst_host, const void *src_dev, size_t bytes);
 int aotk_memset(void *dst_dev, int value, size_t bytes);
+/* Device-to-device copy on the library stream, synchronous (plumbing with no
+ * counterpart in the reference; the benchmark uses it as the known-size copy
+ * that calibrates the HBM traffic counters). */
+int aotk_d2d(void *dst_dev, const void *src_dev, size_t bytes);
 int aotk_sync(void);
 
 /* Bytes per row of `cols` elements (quant.rs:70-73 `Kind::row_bytes`). */
