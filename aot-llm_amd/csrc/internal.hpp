@@ -164,6 +164,11 @@ void launch_attention(float *out, const float *q, const float *k_cache, const fl
                       size_t n_kv_head, size_t head_dim, size_t ctx_rows, size_t pos0, size_t m, size_t window,
                       const int *pos_dev, float *scratch, size_t scratch_bytes, hipStream_t s);
 size_t attention_scratch_bytes(size_t n_head, size_t head_dim, size_t ctx, size_t m);
+// Decode step (one row at *pos_dev or pos0): the q/k/v epilogue of `p`
+// (bias, q/k norms, rope, KV store) fused into the scores, then softmax and
+// output. Writes out [n_head * head_dim].
+void launch_attention_decode(float *out, const QkvPost &p, size_t ctx_rows, size_t pos0, size_t window,
+                             const int *pos_dev, float *scratch, hipStream_t s);
 void launch_add(float *x, const float *y, size_t n, hipStream_t s);
 void launch_rmsnorm_add(float *x, const float *y, const float *w, size_t n, size_t m, float eps, hipStream_t s);
 void launch_argmax(const float *x, size_t n, uint32_t *out_dev, float *scratch, hipStream_t s);

@@ -16,6 +16,10 @@
 #include "internal.hpp"
 
 
+#ifndef MV_TS
+#define MV_TS(i)
+#endif
+
 namespace aotk {
 
 constexpr int MAX_SEG = 3;
@@ -38,22 +42,31 @@ struct MvArgs {
     const float *xf;
 };
 
+// Segment of a global row (constant indices only, so that the kernel
+// arguments stay in scalar registers).
 __device__ __forceinline__ int seg_of(const MvArgs &a, int row, int &local) {
-    int s = 0;
-    local = row;
-    while (s + 1 < a.nseg && local >= a.rows[s]) {
-        local -= a.rows[s];
-        s++;
+    const int r0 = a.rows[0], r1 = a.rows[1];
+    if (a.nseg > 1 && row >= r0) {
+        if (a.nseg > 2 && row >= r0 + r1) {
+            local = row - r0 - r1;
+            return 2;
+        }
+        local = row - r0;
+        return 1;
     }
-    return s;
+    local = row;
+    return 0;
 }
+template <typename T>
+__device__ __forceinline__ T seg_sel(int s, T v0, T v1, T v2) { return s == 0 ? v0 : (s == 1 ? v1 : v2); }
 
 __device__ __forceinline__ void store_row(const MvArgs &a, int grow, int tok, float v) {
     int local;
-    int s = seg_of(a, grow, local);
-    size_t at = (size_t)tok * a.rows[s] + local;
-    float r = a.add[s] ? a.add[s][at] + v : v;
-    a.y[s][at] = r;
+    const int s = seg_of(a, grow, local);
+    const size_t at = (size_t)tok * seg_sel(s, a.rows[0], a.rows[1], a.rows[2]) + local;
+    const float *add = seg_sel(s, a.add[0], a.add[1], a.add[2]);
+    const float r = add ? add[at] + v : v;
+    seg_sel(s, a.y[0], a.y[1], a.y[2])[at] = r;
 }
 
 // --------------------------------------------------------------- K-quants
@@ -126,10 +139,10 @@ __global__ __launch_bounds__(256) void k_mv_kquant(MvArgs a) {
         int local;
         int s = seg_of(a, rvalid[r] ? grow : grow0, local);
         if (KIND == AOTK_Q6_K) {
-            wrow[r] = a.w[s] + (size_t)local * nb * 208;
-            drow[r] = (const uint16_t *)a.w1[s] + (size_t)local * nb;
+            wrow[r] = seg_sel(s, a.w[0], a.w[1], a.w[2]) + (size_t)local * nb * 208;
+            drow[r] = (const uint16_t *)seg_sel(s, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb;
         } else {
-            wrow[r] = a.w[s] + (size_t)local * a.rb;
+            wrow[r] = seg_sel(s, a.w[0], a.w[1], a.w[2]) + (size_t)local * a.rb;
             drow[r] = nullptr;
         }
     }
@@ -256,15 +269,18 @@ struct KqGeom {
     static constexpr int RB = KIND == AOTK_Q4_K ? 144 : (KIND == AOTK_Q5_K ? 176 : 208);  // plane-0 bytes
 };
 
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
+
+// Activation record of one super-block in LDS: qs (256 B), bsums (32 B), d,
+// padded to 304 B so that the lanes of a 16-lane group reading their own
+// super-block's record with 16-byte loads hit disjoint banks.
+constexpr int KQ_REC = 304;
 
 template <int KIND>
-__device__ __forceinline__ float kq_term(const uint4 (&c)[KqGeom<KIND>::CH], float d6, const uint32_t (&y)[64],
-                                         const int (&bs)[16], float yd) {
+__device__ __forceinline__ float kq_term(const uint4 (&c)[KqGeom<KIND>::CH], float d6, const uint8_t *rec) {
+    const float yd = *(const float *)(rec + 288);
+    const uint4 b0 = *(const uint4 *)(rec + 256), b1 = *(const uint4 *)(rec + 272);
+    const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    auto bs = [&](int g) { return (int)(int16_t)((bw[g >> 1] >> (16 * (g & 1))) & 0xFFFFu); };
     int sumi = 0;
     if (KIND == AOTK_Q4_K || KIND == AOTK_Q5_K) {
         constexpr int QC = KIND == AOTK_Q4_K ? 1 : 3;
@@ -279,6 +295,10 @@ __device__ __forceinline__ float kq_term(const uint4 (&c)[KqGeom<KIND>::CH], flo
         for (int jp = 0; jp < 4; jp++) {
             const uint4 q0 = c[QC + 2 * jp], q1 = c[QC + 2 * jp + 1];
             const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            const uint4 l0 = *(const uint4 *)(rec + 64 * jp), l1 = *(const uint4 *)(rec + 64 * jp + 16);
+            const uint4 h0 = *(const uint4 *)(rec + 64 * jp + 32), h1 = *(const uint4 *)(rec + 64 * jp + 48);
+            const uint32_t yl[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+            const uint32_t yh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
             int slo = 0, shi = 0;
 #pragma unroll
             for (int k = 0; k < 8; k++) {
@@ -288,14 +308,15 @@ __device__ __forceinline__ float kq_term(const uint4 (&c)[KqGeom<KIND>::CH], flo
                     lo |= ((hq[k] >> (2 * jp)) & 0x01010101u) << 4;
                     hi |= ((hq[k] >> (2 * jp + 1)) & 0x01010101u) << 4;
                 }
-                slo = dot4(lo, y[16 * jp + k], slo);
-                shi = dot4(hi, y[16 * jp + 8 + k], shi);
+                slo = dot4(lo, yl[k], slo);
+                shi = dot4(hi, yh[k], shi);
             }
             int sc0, m0, sc1, m1;
             scale_min_k4(2 * jp, hdr.y, hdr.z, hdr.w, sc0, m0);
             scale_min_k4(2 * jp + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
             sumi += sc0 * slo + sc1 * shi;
-            summ += m0 * (bs[4 * jp] + bs[4 * jp + 1]) + m1 * (bs[4 * jp + 2] + bs[4 * jp + 3]);
+            summ += m0 * (bs(4 * jp) + bs(4 * jp + 1)) + m1 * (bs(4 * jp + 2) + bs(4 * jp + 3));
+            __builtin_amdgcn_sched_barrier(0);  // bound the live activation registers
         }
         const float dd = f16_to_f32(hdr.x & 0xFFFFu) * yd;
         const float dm = f16_to_f32(hdr.x >> 16) * yd;
@@ -308,91 +329,109 @@ __device__ __forceinline__ float kq_term(const uint4 (&c)[KqGeom<KIND>::CH], flo
             const int n = g >> 3, quarter = (g & 7) >> 1, half = g & 1;
             const uint4 l4 = c[4 * n + 2 * (quarter & 1) + half];
             const uint4 h4 = c[8 + 2 * n + half];
+            const uint4 y4 = *(const uint4 *)(rec + 16 * g);
             const uint32_t lw[4] = {l4.x, l4.y, l4.z, l4.w};
             const uint32_t hw[4] = {h4.x, h4.y, h4.z, h4.w};
+            const uint32_t yw[4] = {y4.x, y4.y, y4.z, y4.w};
             int sg = 0;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 const uint32_t nib = quarter >= 2 ? (lw[k] >> 4) & 0x0F0F0F0Fu : lw[k] & 0x0F0F0F0Fu;
                 const uint32_t v = nib | (((hw[k] >> (2 * quarter)) & 0x03030303u) << 4);
-                sg = dot4(v, y[4 * g + k], sg);
+                sg = dot4(v, yw[k], sg);
             }
             const int sc = (int)(int8_t)((scw[g >> 2] >> (8 * (g & 3))) & 0xFFu);
-            sumi += sc * (sg - 32 * bs[g]);
+            sumi += sc * (sg - 32 * bs(g));
+            if ((g & 3) == 3) __builtin_amdgcn_sched_barrier(0);
         }
         const float dd = d6 * yd;
         return dd * (float)sumi;
     }
 }
 
-template <int KIND>
-__global__ __launch_bounds__(256) void k_mv_kq(MvArgs a, int RL, int G) {
+// PF = 0: one row group per wave (G == 1), register budget for 4 waves per
+// SIMD; PF = 1: G groups per wave with the next group's loads in flight.
+template <int KIND, int PF>
+__global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq(MvArgs a, int RL, int G) {
     using Geo = KqGeom<KIND>;
     constexpr int CH = Geo::CH;
-    __shared__ float sT[4][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ __align__(16) uint8_t sY[64 * KQ_REC];
+    __shared__ __align__(16) float sT[4][256 + 16];  // [wave][row slot * ts + super-block] (+ read slack)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tok = blockIdx.y;
     const int nb = a.nb;
     const int rs = lane / nb, s = lane - rs * nb;
     const bool lane_on = rs < RL;
     const int sa = lane_on ? s : 0;
-    // activation of super-block s
-    uint32_t y[64];
-    int bs[16];
-    {
-        const uint4 *xq = (const uint4 *)(a.xq + (size_t)tok * a.cols + (size_t)sa * 256);
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const uint4 v = xq[k];
-            y[4 * k] = v.x;
-            y[4 * k + 1] = v.y;
-            y[4 * k + 2] = v.z;
-            y[4 * k + 3] = v.w;
-        }
-        const uint4 *bp = (const uint4 *)(a.xbs + ((size_t)tok * nb + sa) * 16);
-        const uint4 b0 = bp[0], b1 = bp[1];
-        const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            bs[2 * k] = (int)(int16_t)(bw[k] & 0xFFFFu);
-            bs[2 * k + 1] = (int)(int16_t)(bw[k] >> 16);
-        }
-    }
-    const float yd = a.xd[(size_t)tok * nb + sa];
     const size_t cs = (size_t)nb * 16;
     const size_t rowb = (size_t)nb * Geo::RB;
     const int group0 = (blockIdx.x * 4 + wave) * G;
+    const int ts = (nb + 3) & ~3;  // row stride of the fold buffer (RL * ts <= 256)
 
-    uint4 cur[CH], nxt[CH];
+    uint4 cur[CH], nxt[PF ? CH : 1];
     float dcur = 0.0f, dnxt = 0.0f;
-    auto load = [&](uint4 (&c)[CH], float &d6, int gi) {
+    auto load = [&](uint4 *c, float &d6, int gi) {
+        // rows past the end load row 0 (valid memory); their results are
+        // never folded
         const int row = (group0 + gi) * RL + rs;
         const bool on = lane_on && row < a.total_rows;
         int local;
         const int sg = seg_of(a, on ? row : 0, local);
-        const uint8_t *wp = a.w[sg] + (size_t)local * rowb + (size_t)sa * 16;
+        const uint8_t *wp = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * rowb + (size_t)sa * 16;
 #pragma unroll
-        for (int k = 0; k < CH; k++) c[k] = on ? *(const uint4 *)(wp + k * cs) : make_uint4(0, 0, 0, 0);
-        if (KIND == AOTK_Q6_K) d6 = on ? f16_to_f32(((const uint16_t *)a.w1[sg])[(size_t)local * nb + sa]) : 0.0f;
+        for (int k = 0; k < CH; k++) c[k] = *(const uint4 *)(wp + k * cs);
+        if (KIND == AOTK_Q6_K)
+            d6 = f16_to_f32(((const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]))[(size_t)local * nb + sa]);
     };
-    load(cur, dcur, 0);
-    for (int gi = 0; gi < G; gi++) {
+    MV_TS(0);
+    load(cur, dcur, 0);  // weights first: the longest latency
+    // stage this token's Q8_K activation in LDS
+    {
+        const uint4 *xq = (const uint4 *)(a.xq + (size_t)tok * a.cols);
+        for (int i = tid; i < nb * 16; i += 256) *(uint4 *)(sY + (i >> 4) * KQ_REC + (i & 15) * 16) = xq[i];
+        const uint4 *xb = (const uint4 *)(a.xbs + (size_t)tok * nb * 16);
+        for (int i = tid; i < nb * 2; i += 256) *(uint4 *)(sY + (i >> 1) * KQ_REC + 256 + (i & 1) * 16) = xb[i];
+        for (int i = tid; i < nb; i += 256) *(float *)(sY + i * KQ_REC + 288) = a.xd[(size_t)tok * nb + i];
+    }
+    __syncthreads();
+    MV_TS(1);
+    const uint8_t *rec = sY + sa * KQ_REC;
+    const int ng = PF ? G : 1;
+    for (int gi = 0; gi < ng; gi++) {
         const int gr0 = (group0 + gi) * RL;
         if (gr0 >= a.total_rows) break;
-        if (gi + 1 < G) load(nxt, dnxt, gi + 1);
-        const float term = kq_term<KIND>(cur, dcur, y, bs, yd);
-        sT[wave][lane] = term;
+        if (PF && gi + 1 < G) load(nxt, dnxt, gi + 1);
+        const float term = kq_term<KIND>(cur, dcur, rec);
+        MV_TS(2 + 2 * gi);
+        if (lane_on) sT[wave][rs * ts + s] = term;
         wave_lds_sync();
         if (lane < RL && gr0 + lane < a.total_rows) {
-            const float *tp = &sT[wave][lane * nb];
+            // fold in super-block order; the terms are read 16 at a time
+            // ahead of the dependent adds
+            const float4 *tp = (const float4 *)&sT[wave][lane * ts];
             float acc = 0.0f;
-            for (int k = 0; k < nb; k++) acc = acc + tp[k];
+            for (int k0 = 0; k0 < nb; k0 += 16) {
+                float t[16];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 v = tp[k0 / 4 + q];
+                    t[4 * q] = v.x;
+                    t[4 * q + 1] = v.y;
+                    t[4 * q + 2] = v.z;
+                    t[4 * q + 3] = v.w;
+                }
+                const int n = nb - k0 < 16 ? nb - k0 : 16;
+#pragma unroll
+                for (int q = 0; q < 16; q++)
+                    if (q < n) acc = acc + t[q];
+            }
             store_row(a, gr0 + lane, tok, acc);
         }
         wave_lds_sync();
-        if (gi + 1 < G) {
+        MV_TS(3 + 2 * gi);
+        if (PF && gi + 1 < G) {
 #pragma unroll
-            for (int k = 0; k < CH; k++) cur[k] = nxt[k];
+            for (int k = 0; k < CH; k++) cur[k] = nxt[PF ? k : 0];
             dcur = dnxt;
         }
     }
@@ -434,18 +473,18 @@ __global__ __launch_bounds__(256) void k_mv_q80(MvArgs a) {
                 const uint4 y0 = *(const uint4 *)(xq + (size_t)bi * 32);
                 const uint4 y1 = *(const uint4 *)(xq + (size_t)bi * 32 + 16);
                 const uint32_t yw[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
-                const float dw = f16_to_f32(((const uint16_t *)a.w1[s])[blk]);
+                const float dw = f16_to_f32(((const uint16_t *)seg_sel(s, a.w1[0], a.w1[1], a.w1[2]))[blk]);
                 D = dw * xd[bi];
                 if (KIND == AOTK_Q8_0) {
-                    const uint4 w0 = *(const uint4 *)(a.w[s] + blk * 32);
-                    const uint4 w1 = *(const uint4 *)(a.w[s] + blk * 32 + 16);
+                    const uint4 w0 = *(const uint4 *)(seg_sel(s, a.w[0], a.w[1], a.w[2]) + blk * 32);
+                    const uint4 w1 = *(const uint4 *)(seg_sel(s, a.w[0], a.w[1], a.w[2]) + blk * 32 + 16);
                     const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
                     for (int l = 0; l < 8; l++) P[l] = (float)dot4(ww[l], yw[l], 0);
                 } else {
-                    const uint4 w0 = *(const uint4 *)(a.w[s] + blk * 16);
+                    const uint4 w0 = *(const uint4 *)(seg_sel(s, a.w[0], a.w[1], a.w[2]) + blk * 16);
                     const uint32_t nw[4] = {w0.x, w0.y, w0.z, w0.w};
                     uint32_t qh = 0;
-                    if (KIND == AOTK_Q5_0) qh = ((const uint32_t *)a.w2[s])[blk];
+                    if (KIND == AOTK_Q5_0) qh = ((const uint32_t *)seg_sel(s, a.w2[0], a.w2[1], a.w2[2]))[blk];
                     for (int l = 0; l < 8; l++) {
                         uint32_t v = l < 4 ? (nw[l] & 0x0F0F0F0Fu) : ((nw[l - 4] >> 4) & 0x0F0F0F0Fu);
                         int off;
@@ -498,7 +537,7 @@ __global__ __launch_bounds__(256) void k_mv_float(MvArgs a) {
     const bool valid = grow < a.total_rows;
     int local;
     const int s = seg_of(a, valid ? grow : 0, local);
-    const uint8_t *row = a.w[s] + (size_t)local * a.rb;
+    const uint8_t *row = seg_sel(s, a.w[0], a.w[1], a.w[2]) + (size_t)local * a.rb;
     const float *x = a.xf + (size_t)tok * a.cols;
     const size_t n8 = a.cols / 8;
     float acc = 0.0f;
@@ -564,11 +603,13 @@ static void launch_kq(const MvArgs &a, dim3 grid, hipStream_t s) {
     if (a.nb <= 64) {
         int RL = 1;
         while (RL * 2 * a.nb <= 64) RL *= 2;
+        // all waves resident in one round (3 waves per SIMD on 256 CUs),
+        // each doing G row groups
         const int groups = (a.total_rows + RL - 1) / RL;
-        int G = (groups + 2047) / 2048;
-        G = G < 1 ? 1 : (G > 8 ? 8 : G);
+        int G = (groups + 3071) / 3072;
+        G = G > 8 ? 8 : G;
         grid.x = (unsigned)((groups + 4 * G - 1) / (4 * G));
-        k_mv_kq<KIND><<<grid, 256, 0, s>>>(a, RL, G);
+        k_mv_kq<KIND, 1><<<grid, 256, 0, s>>>(a, RL, G);
     } else {
         grid.x = (unsigned)((a.total_rows + 7) / 8);
         k_mv_kquant<KIND, 2><<<grid, 256, 0, s>>>(a);

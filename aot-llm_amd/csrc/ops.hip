@@ -390,116 +390,200 @@ __global__ __launch_bounds__(512) void k_attn_scores(AttnArgs a) {
     a.prob[(i * a.n_head + (size_t)(kvh * gqa + hg)) * a.span + (start + lane - t0)] = s * a.scale;
 }
 
-// Softmax per (row, head), staged in LDS (span <= ATT_MAX_SPAN).
-constexpr int ATT_MAX_SPAN = 16384;
-__global__ __launch_bounds__(SEQ_T) void k_attn_softmax(AttnArgs a) {
-    __shared__ __align__(16) float e[ATT_MAX_SPAN + 64];
-    __shared__ SeqScratch S;
-    __shared__ float red[SEQ_T / 64];
-    __shared__ float bc;
-    const int h = blockIdx.x;
-    const size_t i = blockIdx.y;
-    size_t t0, n;
-    row_range(a, i, t0, n);
-    const int cnt = (int)(n - t0);
-    // scores in the padded chunk layout of the exact sum when it applies
-    const bool exact = cnt <= SEQ_MAX_N;
-    const int C = seq_chunk(cnt);
-    auto at = [&](int t) { return exact ? seq_idx(t, C) : t; };
-    float *p = a.prob + (i * a.n_head + h) * a.span;
-    float mx = -INFINITY;
-    for (int t = threadIdx.x; t < cnt; t += blockDim.x) {
-        float v = p[t];
-        e[at(t)] = v;
-        mx = fmaxf(mx, v);
+// One wave's share of the q/k/v epilogue for one head vector (decode):
+// bias, rmsnorm_heads (sequential sum of squares by lane 0), rope with the
+// position's table row; the result is left in `hv` (LDS, hd floats).
+__device__ __forceinline__ void head_post_wave(float *hv, const float *src, const float *bias, const float *nw,
+                                               const float *cs_row, int hd, int rot_dim, int neox, float eps) {
+    const int lane = threadIdx.x & 63;
+    for (int e = lane; e < hd; e += 64) {
+        float v = src[e];
+        if (bias) v = v + bias[e];
+        hv[e] = v;
     }
-    mx = wave_max(mx);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    {
-        const int lane = threadIdx.x & 63;
-        mx = wave_max(lane < SEQ_T / 64 ? red[lane] : -INFINITY);
+    wave_lds_sync();
+    if (nw) {
+        float ss = 0.0f;
+        if (lane == 0) ss = seq_sum_lds<true>(hv, hd);
+        ss = __shfl(ss, 0, 64);
+        const float r = 1.0f / sqrtf(ss / (float)hd + eps);
+        for (int e = lane; e < hd; e += 64) hv[e] = hv[e] * r * nw[e];
+        wave_lds_sync();
     }
-    for (int t = threadIdx.x; t < cnt; t += blockDim.x) e[at(t)] = aotk_expf(e[at(t)] - mx);
-    __syncthreads();
-    float sum;
-    if (exact) {
-        sum = exact_seq_sum(e, cnt, S);
-    } else {
-        if (threadIdx.x == 0) bc = seq_sum_lds<false>(e, cnt);
-        __syncthreads();
-        sum = bc;
+    const int half = rot_dim / 2;
+    for (int t = lane; t < half; t += 64) {
+        const float c = cs_row[2 * t], sn = cs_row[2 * t + 1];
+        const int ia = neox ? t : 2 * t, ib = neox ? t + half : 2 * t + 1;
+        const float x0 = hv[ia], x1 = hv[ib];
+        hv[ia] = x0 * c - x1 * sn;
+        hv[ib] = x0 * sn + x1 * c;
     }
-    const float inv = 1.0f / sum;
-    for (int t = threadIdx.x; t < cnt; t += blockDim.x) p[t] = e[at(t)] * inv;
+    wave_lds_sync();
 }
 
-// Output: block = one wave, AO_DB dims of one head. Products p_t * v_t,d
-// of a chunk of AO_TC positions are formed by the whole wave (float4 V
-// loads, 16 positions per pass) into LDS; lanes 0..AO_DB-1 then add them in
-// position order. The next chunk's loads are in flight during the adds.
-constexpr int AO_DB = 16;
-constexpr int AO_TC = 256;
-__global__ __launch_bounds__(64) void k_attn_out(AttnArgs a) {
-    __shared__ __align__(16) float buf[2][AO_TC * AO_DB];
-    constexpr int NP = AO_TC / 16;
-    const int lane = threadIdx.x;
-    const int hd = a.hd;
-    const int per_head = hd / AO_DB;
-    const int h = blockIdx.x / per_head, d0 = (blockIdx.x % per_head) * AO_DB;
+// Decode (one row) scores with the q/k/v epilogue fused in: block = (kv head,
+// chunk of ATT_CH positions), (gqa + 1) waves. Waves 0..gqa-1 post-process
+// their query head; wave gqa post-processes the new k (and v) of the kv head
+// and, in the block whose chunk holds the position, stores both into the
+// cache. The chunk's K rows are staged in LDS (the new position's row from
+// the post-processed k), then thread (query head, position) runs its dot
+// product sequentially over the head dimension.
+template <int HD>
+__global__ __launch_bounds__(576) void k_attn_qk_decode(AttnArgs a, QkvPost p) {
+    constexpr int KS = HD + 1;
+    __shared__ float sk[ATT_CH * KS];
+    __shared__ __align__(16) float sq[ATT_MAX_GQA + 1][HD];
+    const int gqa = a.n_head / a.n_kv_head;
+    const int lane = threadIdx.x & 63, hg = threadIdx.x >> 6;
+    const int kvh = blockIdx.x, c = blockIdx.y;
+    size_t t0, n;
+    row_range(a, 0, t0, n);
+    const size_t pos = n - 1;
+    const size_t start = t0 + (size_t)c * ATT_CH;
+    if (start >= n) return;
+    const int rows = (int)min((size_t)ATT_CH, n - start);
+    const size_t kv = (size_t)a.n_kv_head * HD;
+    const float *cs_row = p.cs + pos * p.rot_dim;
+    if (hg < gqa) {
+        const int h = kvh * gqa + hg;
+        head_post_wave(sq[hg], p.q + (size_t)h * HD, p.bq ? p.bq + (size_t)h * HD : nullptr, p.q_norm, cs_row, HD,
+                       (int)p.rot_dim, p.neox, p.eps);
+    } else {
+        float *kn = sq[ATT_MAX_GQA];
+        head_post_wave(kn, p.k + (size_t)kvh * HD, p.bk ? p.bk + (size_t)kvh * HD : nullptr, p.k_norm, cs_row, HD,
+                       (int)p.rot_dim, p.neox, p.eps);
+        if (pos >= start && pos < start + ATT_CH) {
+            float *kc = p.k_cache + pos * kv + (size_t)kvh * HD;
+            float *vc = p.v_cache + pos * kv + (size_t)kvh * HD;
+            for (int e = lane; e < HD; e += 64) {
+                kc[e] = kn[e];
+                float v = p.v[(size_t)kvh * HD + e];
+                if (p.bv) v = v + p.bv[(size_t)kvh * HD + e];
+                vc[e] = v;
+            }
+        }
+    }
+    // K rows of the chunk (the new position from the post-processed k)
+    const float *kb = a.k_cache + start * kv + (size_t)kvh * HD;
+    constexpr int R4 = HD / 4;
+    const int nthreads = (gqa + 1) * 64;
+    for (int idx = threadIdx.x; idx < rows * R4; idx += nthreads) {
+        const int r = idx / R4, c4 = idx % R4;
+        float4 k4;
+        if (start + r == pos) k4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        else k4 = *(const float4 *)(kb + (size_t)r * kv + 4 * c4);
+        float *d = sk + r * KS + 4 * c4;
+        d[0] = k4.x;
+        d[1] = k4.y;
+        d[2] = k4.z;
+        d[3] = k4.w;
+    }
+    __syncthreads();
+    if (pos >= start && pos < start + ATT_CH) {  // the new row
+        const int r = (int)(pos - start);
+        for (int e = threadIdx.x; e < HD; e += nthreads) sk[r * KS + e] = sq[ATT_MAX_GQA][e];
+        __syncthreads();
+    }
+    if (hg >= gqa || lane >= rows) return;
+    const float *kr = sk + lane * KS;
+    const float *qq = sq[hg];
+    float sc = 0.0f;
+#pragma unroll 16
+    for (int d = 0; d < HD; d++) sc += qq[d] * kr[d];
+    a.prob[(size_t)(kvh * gqa + hg) * a.span + (start + lane - t0)] = sc * a.scale;
+}
+
+// Softmax and output per (row, head): block of SEQ_T threads.
+//   softmax (ops.rs:98-112): max, glibc-matched exp, the sequential sum
+//   (exact parallel replay when the span is <= SEQ_MAX_N), multiply by 1/sum;
+//   output (ops.rs:209-215): chunks of SV_CP(HD) positions: all threads form
+//   the products p_t * v_t,d into LDS (float4 V loads), then thread d adds
+//   them in position order while the others form the next chunk.
+constexpr int ATT_MAX_SPAN = 16384;
+constexpr int SV_BUF = 8192;  // floats per product buffer
+template <int HD>
+__global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
+    constexpr int CP = SV_BUF / HD;
+    __shared__ __align__(16) float e[ATT_MAX_SPAN + 64];
+    __shared__ __align__(16) uint8_t ubuf[sizeof(SeqScratch) > 2 * SV_BUF * 4 ? sizeof(SeqScratch) : 2 * SV_BUF * 4];
+    __shared__ float red[SEQ_T / 64];
+    __shared__ float bc;
+    SeqScratch &S = *reinterpret_cast<SeqScratch *>(ubuf);
+    float *prod = reinterpret_cast<float *>(ubuf);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int h = blockIdx.x;
     const size_t i = blockIdx.y;
     const int gqa = a.n_head / a.n_kv_head;
     const int kvh = h / gqa;
     size_t t0, n;
     row_range(a, i, t0, n);
     const int cnt = (int)(n - t0);
-    const size_t kv = (size_t)a.n_kv_head * hd;
-    const float *p = a.prob + (i * a.n_head + h) * a.span;
-    const float *vb = a.v_cache + t0 * kv + (size_t)kvh * hd + d0 + 4 * (lane & 3);
-    const int r = lane >> 2;
-    float4 R[NP];
-    float Pp[NP];
-    auto issue = [&](int base) {
-#pragma unroll
-        for (int j = 0; j < NP; j++) {
-            const int t = base + r + 16 * j;
-            if (t < cnt) {
-                R[j] = *(const float4 *)(vb + (size_t)t * kv);
-                Pp[j] = p[t];
-            } else {
-                R[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                Pp[j] = 0.0f;
-            }
-        }
-    };
-    const int nch = (cnt + AO_TC - 1) / AO_TC;
+    const bool exact = cnt <= SEQ_MAX_N;
+    const int C = seq_chunk(cnt);
+    auto at = [&](int t) { return exact ? seq_idx(t, C) : t; };
+    const float *ps = a.prob + (i * a.n_head + h) * a.span;
+    float mx = -INFINITY;
+    for (int t = tid; t < cnt; t += SEQ_T) {
+        const float v = ps[t];
+        e[at(t)] = v;
+        mx = fmaxf(mx, v);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = wave_max(lane < SEQ_T / 64 ? red[lane] : -INFINITY);
+    for (int t = tid; t < cnt; t += SEQ_T) e[at(t)] = aotk_expf(e[at(t)] - mx);
+    __syncthreads();
+    float sum;
+    if (exact) {
+        sum = exact_seq_sum(e, cnt, S);
+    } else {
+        if (tid == 0) bc = seq_sum_lds<false>(e, cnt);
+        __syncthreads();
+        sum = bc;
+    }
+    const float inv = 1.0f / sum;
+    for (int t = tid; t < cnt; t += SEQ_T) e[at(t)] = e[at(t)] * inv;
+    __syncthreads();  // the sum's scratch is reused for the products below
+    const size_t kv = (size_t)a.n_kv_head * HD;
+    const float *vb = a.v_cache + t0 * kv + (size_t)kvh * HD;
+    constexpr int R4 = HD / 4;
     float o = 0.0f;
-    issue(0);
+    const int nch = (cnt + CP - 1) / CP;
     for (int c = 0; c < nch; c++) {
-        float *b = buf[c & 1];
-#pragma unroll
-        for (int j = 0; j < NP; j++) {
-            const float pj = Pp[j];
-            *(float4 *)(b + (r + 16 * j) * AO_DB + 4 * (lane & 3)) =
-                make_float4(pj * R[j].x, pj * R[j].y, pj * R[j].z, pj * R[j].w);
+        float *buf = prod + (c & 1) * SV_BUF;
+        const int base = c * CP;
+        const int rows = min(CP, cnt - base);
+        for (int idx = tid; idx < rows * R4; idx += SEQ_T) {
+            const int r = idx / R4, c4 = idx % R4;
+            const float4 v4 = *(const float4 *)(vb + (size_t)(base + r) * kv + 4 * c4);
+            const float pt = e[at(base + r)];
+            *(float4 *)(buf + r * HD + 4 * c4) = make_float4(pt * v4.x, pt * v4.y, pt * v4.z, pt * v4.w);
         }
         __syncthreads();
-        if (c + 1 < nch) issue((c + 1) * AO_TC);
-        const int len = min(AO_TC, cnt - c * AO_TC);
-        if (lane < AO_DB) {
-            const float *bp = b + lane;
-            int t = 0;
-            for (; t + 16 <= len; t += 16) {
+        if (tid < HD) {
+            const float *bp = buf + tid;
+            int r = 0;
+            for (; r + 16 <= rows; r += 16) {
                 float v[16];
 #pragma unroll
-                for (int k = 0; k < 16; k++) v[k] = bp[(t + k) * AO_DB];
+                for (int k = 0; k < 16; k++) v[k] = bp[(r + k) * HD];
 #pragma unroll
                 for (int k = 0; k < 16; k++) o += v[k];
             }
-            for (; t < len; t++) o += bp[t * AO_DB];
+            for (; r < rows; r++) o += bp[r * HD];
         }
     }
-    if (lane < AO_DB) a.out[i * (size_t)a.n_head * hd + (size_t)h * hd + d0 + lane] = o;
+    if (tid < HD) a.out[i * (size_t)a.n_head * HD + (size_t)h * HD + tid] = o;
+}
+
+static void launch_sv(const AttnArgs &a, size_t head_dim, size_t m, hipStream_t s) {
+    dim3 g((unsigned)a.n_head, (unsigned)m);
+    switch (head_dim) {
+    case 64: k_attn_sv<64><<<g, SEQ_T, 0, s>>>(a); break;
+    case 128: k_attn_sv<128><<<g, SEQ_T, 0, s>>>(a); break;
+    default: k_attn_sv<256><<<g, SEQ_T, 0, s>>>(a); break;
+    }
 }
 
 size_t attention_scratch_bytes(size_t n_head, size_t head_dim, size_t ctx, size_t m) {
@@ -507,10 +591,9 @@ size_t attention_scratch_bytes(size_t n_head, size_t head_dim, size_t ctx, size_
     return align_up(m * n_head * align_up(ctx, 4) * 4, 256);
 }
 
-void launch_attention(float *out, const float *q, const float *k_cache, const float *v_cache, size_t n_head,
-                      size_t n_kv_head, size_t head_dim, size_t ctx_rows, size_t pos0, size_t m, size_t window,
-                      const int *pos_dev, float *scratch, size_t scratch_bytes, hipStream_t s) {
-    (void)scratch_bytes;
+static AttnArgs attn_args(float *out, const float *q, const float *k_cache, const float *v_cache, size_t n_head,
+                          size_t n_kv_head, size_t head_dim, size_t ctx_rows, size_t pos0, size_t window,
+                          const int *pos_dev, float *scratch) {
     AttnArgs a;
     a.out = out;
     a.q = q;
@@ -525,6 +608,15 @@ void launch_attention(float *out, const float *q, const float *k_cache, const fl
     a.window = window;
     a.pos_dev = pos_dev;
     a.scale = 1.0f / sqrtf((float)head_dim);
+    return a;
+}
+
+void launch_attention(float *out, const float *q, const float *k_cache, const float *v_cache, size_t n_head,
+                      size_t n_kv_head, size_t head_dim, size_t ctx_rows, size_t pos0, size_t m, size_t window,
+                      const int *pos_dev, float *scratch, size_t scratch_bytes, hipStream_t s) {
+    (void)scratch_bytes;
+    AttnArgs a = attn_args(out, q, k_cache, v_cache, n_head, n_kv_head, head_dim, ctx_rows, pos0, window, pos_dev,
+                           scratch);
     size_t span = window > 0 && window < ctx_rows ? window : ctx_rows;
     dim3 grid((unsigned)n_kv_head, (unsigned)((span + ATT_CH - 1) / ATT_CH), (unsigned)m);
     const unsigned threads = (unsigned)(64 * (n_head / n_kv_head));
@@ -533,8 +625,22 @@ void launch_attention(float *out, const float *q, const float *k_cache, const fl
     case 128: k_attn_scores<128><<<grid, threads, 0, s>>>(a); break;
     default: k_attn_scores<256><<<grid, threads, 0, s>>>(a); break;
     }
-    k_attn_softmax<<<dim3((unsigned)n_head, (unsigned)m), SEQ_T, 0, s>>>(a);
-    k_attn_out<<<dim3((unsigned)(n_head * head_dim / AO_DB), (unsigned)m), 64, 0, s>>>(a);
+    launch_sv(a, head_dim, m, s);
+}
+
+void launch_attention_decode(float *out, const QkvPost &p, size_t ctx_rows, size_t pos0, size_t window,
+                             const int *pos_dev, float *scratch, hipStream_t s) {
+    AttnArgs a = attn_args(out, p.q, p.k_cache, p.v_cache, p.n_head, p.n_kv_head, p.head_dim, ctx_rows, pos0, window,
+                           pos_dev, scratch);
+    size_t span = window > 0 && window < ctx_rows ? window : ctx_rows;
+    dim3 grid((unsigned)p.n_kv_head, (unsigned)((span + ATT_CH - 1) / ATT_CH), 1);
+    const unsigned threads = (unsigned)(64 * (p.n_head / p.n_kv_head + 1));
+    switch (p.head_dim) {
+    case 64: k_attn_qk_decode<64><<<grid, threads, 0, s>>>(a, p); break;
+    case 128: k_attn_qk_decode<128><<<grid, threads, 0, s>>>(a, p); break;
+    default: k_attn_qk_decode<256><<<grid, threads, 0, s>>>(a, p); break;
+    }
+    launch_sv(a, p.head_dim, 1, s);
 }
 
 // ------------------------------------------------------------ elementwise

@@ -916,10 +916,14 @@ static void run_layers(aotk_state *st, size_t m, size_t pos0, const int *pos_dev
         p.rot_dim = d.rot_dim;
         p.neox = f.rope_neox;
         p.eps = d.eps;
-        launch_qkv_post(p, m, pos0, pos_dev, s);
         size_t window = L.local_attn ? d.swa_window : 0;
-        launch_attention(st->xb, st->q, kc, vc, d.n_head, d.n_kv_head, d.head_dim, st->ctx, pos0, m, window, pos_dev,
-                         st->attn_ws, st->attn_ws_bytes, s);
+        if (m == 1) {
+            launch_attention_decode(st->xb, p, st->ctx, pos0, window, pos_dev, st->attn_ws, s);
+        } else {
+            launch_qkv_post(p, m, pos0, pos_dev, s);
+            launch_attention(st->xb, st->q, kc, vc, d.n_head, d.n_kv_head, d.head_dim, st->ctx, pos0, m, window,
+                             pos_dev, st->attn_ws, st->attn_ws_bytes, s);
+        }
         if (activation(L.wo.kind) != ACT_F32) launch_quant_f32(st->xb, qd, m, outs_for(st, {L.wo.kind}, nullptr), s);
         if (f.post_norms) {
             launch_matvec(L.wo, act_for(st, L.wo.kind, st->xb), m, st->xb2, nullptr, s);
