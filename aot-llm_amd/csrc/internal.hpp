@@ -134,7 +134,8 @@ void launch_ref_to_q8_0(const aotk_block_q8_0 *in, size_t n, size_t rows, ActQ8_
 // `add` (may be null) is added to the result (fused residual add).
 void launch_matvec(const DevWeight &w, const void *x_act, size_t m, float *y, const float *add, hipStream_t s);
 // Up to three matrices sharing kind/cols/input in one launch (q/k/v, gate/up).
-void launch_matvec_multi(int n, const DevWeight *const ws[], float *const ys[], const void *x_act, hipStream_t s);
+void launch_matvec_multi(int n, const DevWeight *const ws[], float *const ys[], const void *x_act, size_t m,
+                         hipStream_t s);
 
 // ops.hip
 struct RmsOut {

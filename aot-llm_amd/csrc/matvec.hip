@@ -664,9 +664,10 @@ void launch_matvec(const DevWeight &w, const void *x_act, size_t m, float *y, co
     launch_args(w.kind, a, m, s);
 }
 
-void launch_matvec_multi(int n, const DevWeight *const ws[], float *const ys[], const void *x_act, hipStream_t s) {
+void launch_matvec_multi(int n, const DevWeight *const ws[], float *const ys[], const void *x_act, size_t m,
+                         hipStream_t s) {
     MvArgs a = make_args(n, ws, ys, nullptr, x_act);
-    launch_args(ws[0]->kind, a, 1, s);
+    launch_args(ws[0]->kind, a, m, s);
 }
 
 }  // namespace aotk

@@ -13,6 +13,7 @@
 #include "formats.hpp"
 #include "internal.hpp"
 #include "seqsum.hpp"
+#include "actfn.hpp"
 
 namespace aotk {
 
@@ -81,59 +82,6 @@ __device__ float seq_sumsq_lds(const float *v, int n, float *bcast) {
     if (threadIdx.x == 0) *bcast = seq_sum_lds<true>(v, n);
     __syncthreads();
     return *bcast;
-}
-
-// Quantize 256 values held 4 per lane (element 4*lane + k) of one wave into
-// the Q8_K block `blk` (quant.rs:248-283) and/or the 8 Q8_0 blocks
-// 8*blk .. 8*blk+7 (quant.rs:231-245).
-__device__ void quant256(const float v[4], int lane, size_t blk, ActQ8K q8k, ActQ8_0 q80) {
-    if (q8k.qs) {
-        float amax = 0.0f;
-        int idx = 0x7fffffff;
-        for (int k = 0; k < 4; k++) {
-            float a = fabsf(v[k]);
-            if (a > amax) { amax = a; idx = lane * 4 + k; }
-        }
-        for (int m = 1; m < 64; m <<= 1) {
-            float oa = shfl_xor(amax, m);
-            int oi = shfl_xor(idx, m);
-            if (oa > amax || (oa == amax && oi < idx)) { amax = oa; idx = oi; }
-        }
-        int src_lane = (idx == 0x7fffffff) ? 0 : idx >> 2, sk = idx & 3;
-        float c0 = __shfl(v[0], src_lane, 64), c1 = __shfl(v[1], src_lane, 64);
-        float c2 = __shfl(v[2], src_lane, 64), c3 = __shfl(v[3], src_lane, 64);
-        float max = sk == 0 ? c0 : (sk == 1 ? c1 : (sk == 2 ? c2 : c3));
-        uint32_t packed = 0;
-        int sum = 0;
-        float d = 0.0f;
-        if (amax != 0.0f) {
-            float iscale = -127.0f / max;
-            for (int k = 0; k < 4; k++) {
-                int t = round_i(iscale * v[k]);
-                t = t > 127 ? 127 : t;
-                packed |= (uint32_t)(t & 0xFF) << (8 * k);
-                sum += (int8_t)t;
-            }
-            d = 1.0f / iscale;
-        }
-        ((uint32_t *)(q8k.qs + blk * 256))[lane] = packed;
-        sum += shfl_xor(sum, 1);
-        sum += shfl_xor(sum, 2);
-        if ((lane & 3) == 0) q8k.bsums[blk * 16 + lane / 4] = (int16_t)sum;
-        if (lane == 0) q8k.d[blk] = d;
-    }
-    if (q80.qs) {
-        float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        amax = fmaxf(amax, shfl_xor(amax, 1));
-        amax = fmaxf(amax, shfl_xor(amax, 2));
-        amax = fmaxf(amax, shfl_xor(amax, 4));
-        float d = amax / 127.0f;
-        float id = d != 0.0f ? 1.0f / d : 0.0f;
-        uint32_t packed = 0;
-        for (int k = 0; k < 4; k++) packed |= (uint32_t)(clampi(round_i(v[k] * id), -127, 127) & 0xFF) << (8 * k);
-        ((uint32_t *)(q80.qs + blk * 256))[lane] = packed;
-        if ((lane & 7) == 0) q80.d[blk * 8 + lane / 8] = d;
-    }
 }
 
 __device__ __forceinline__ ActQ8K q8k_row(ActQ8K a, size_t row, size_t n) {
@@ -208,12 +156,6 @@ void launch_quant_f32(const float *x, size_t n, size_t m, RmsOut out, hipStream_
 }
 
 // silu_mul / gelu_mul (ops.rs:115-134) then quantization; one wave per 256.
-__device__ __forceinline__ float silu_f(float v, float b) { return v / (1.0f + aotk_expf(-v)) * b; }
-__device__ __forceinline__ float gelu_f(float v) {
-    const float k = (float)1.1283791670955126 / (float)1.4142135623730951;
-    return 0.5f * v * (1.0f + aotk_tanhf(k * (v + 0.044715f * v * v * v)));
-}
-
 __global__ void k_glu_quant(const float *__restrict__ gate, const float *__restrict__ up, int n, size_t total_blk, int gelu,
                             RmsOut out) {
     const int lane = threadIdx.x & 63;
@@ -493,17 +435,27 @@ __global__ __launch_bounds__(576) void k_attn_qk_decode(AttnArgs a, QkvPost p) {
     a.prob[(size_t)(kvh * gqa + hg) * a.span + (start + lane - t0)] = sc * a.scale;
 }
 
-// Softmax and output per (row, head): block of SEQ_T threads.
-//   softmax (ops.rs:98-112): max, glibc-matched exp, the sequential sum
-//   (exact parallel replay when the span is <= SEQ_MAX_N), multiply by 1/sum;
-//   output (ops.rs:209-215): chunks of SV_CP(HD) positions: all threads form
-//   the products p_t * v_t,d into LDS (float4 V loads), then thread d adds
-//   them in position order while the others form the next chunk.
+// Softmax and output per (row, head, group of SV_DB dims): block of SEQ_T
+// threads.
+//   softmax (ops.rs:98-112): max, glibc-matched exp, the sequential sum (one
+//   thread for short spans, the exact parallel replay for spans of
+//   SV_SEQ_MIN..SEQ_MAX_N), multiply by 1/sum; the blocks of one head repeat
+//   it identically;
+//   output (ops.rs:209-215): chunks of SV_CP positions: all threads form the
+//   products p_t * v_t,d into LDS (float4 V loads issued SV_PD chunks ahead),
+//   then thread d adds them in position order while the others form the
+//   next chunk.
+#ifndef ATT_TS
+#define ATT_TS(i)
+#endif
 constexpr int ATT_MAX_SPAN = 16384;
-constexpr int SV_BUF = 8192;  // floats per product buffer
+constexpr int SV_BUF = 8192;      // floats per product buffer
+constexpr int SV_DB = 32;         // dims per block
+constexpr int SV_SEQ_MIN = 2048;  // shorter spans are summed by one thread
 template <int HD>
 __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
-    constexpr int CP = SV_BUF / HD;
+    constexpr int DB = SV_DB;
+    constexpr int CP = SV_BUF / DB;
     __shared__ __align__(16) float e[ATT_MAX_SPAN + 64];
     __shared__ __align__(16) uint8_t ubuf[sizeof(SeqScratch) > 2 * SV_BUF * 4 ? sizeof(SeqScratch) : 2 * SV_BUF * 4];
     __shared__ float red[SEQ_T / 64];
@@ -511,17 +463,18 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     SeqScratch &S = *reinterpret_cast<SeqScratch *>(ubuf);
     float *prod = reinterpret_cast<float *>(ubuf);
     const int tid = threadIdx.x, lane = tid & 63;
-    const int h = blockIdx.x;
+    const int h = blockIdx.x / (HD / DB), d0 = (blockIdx.x % (HD / DB)) * DB;
     const size_t i = blockIdx.y;
     const int gqa = a.n_head / a.n_kv_head;
     const int kvh = h / gqa;
     size_t t0, n;
     row_range(a, i, t0, n);
     const int cnt = (int)(n - t0);
-    const bool exact = cnt <= SEQ_MAX_N;
+    const bool exact = cnt >= SV_SEQ_MIN && cnt <= SEQ_MAX_N;
     const int C = seq_chunk(cnt);
     auto at = [&](int t) { return exact ? seq_idx(t, C) : t; };
     const float *ps = a.prob + (i * a.n_head + h) * a.span;
+    ATT_TS(0);
     float mx = -INFINITY;
     for (int t = tid; t < cnt; t += SEQ_T) {
         const float v = ps[t];
@@ -532,8 +485,10 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     if (lane == 0) red[tid >> 6] = mx;
     __syncthreads();
     mx = wave_max(lane < SEQ_T / 64 ? red[lane] : -INFINITY);
+    ATT_TS(1);
     for (int t = tid; t < cnt; t += SEQ_T) e[at(t)] = aotk_expf(e[at(t)] - mx);
     __syncthreads();
+    ATT_TS(2);
     float sum;
     if (exact) {
         sum = exact_seq_sum(e, cnt, S);
@@ -545,40 +500,65 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     const float inv = 1.0f / sum;
     for (int t = tid; t < cnt; t += SEQ_T) e[at(t)] = e[at(t)] * inv;
     __syncthreads();  // the sum's scratch is reused for the products below
+    ATT_TS(3);
     const size_t kv = (size_t)a.n_kv_head * HD;
-    const float *vb = a.v_cache + t0 * kv + (size_t)kvh * HD;
-    constexpr int R4 = HD / 4;
+    const float *vb = a.v_cache + t0 * kv + (size_t)kvh * HD + d0;
+    constexpr int R4 = DB / 4;
+    static_assert(CP * R4 == 2 * SEQ_T, "two float4 per thread per chunk");
+    // V loads run SV_PD chunks ahead of the products (a register ring)
+    constexpr int PD = 8;
+    float4 ring[PD][2];
+    auto issue = [&](float4 (&dst)[2], int c) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int idx = tid + k * SEQ_T;
+            const int t = c * CP + idx / R4;
+            dst[k] = t < cnt ? *(const float4 *)(vb + (size_t)t * kv + 4 * (idx % R4)) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
     float o = 0.0f;
     const int nch = (cnt + CP - 1) / CP;
-    for (int c = 0; c < nch; c++) {
-        float *buf = prod + (c & 1) * SV_BUF;
-        const int base = c * CP;
-        const int rows = min(CP, cnt - base);
-        for (int idx = tid; idx < rows * R4; idx += SEQ_T) {
-            const int r = idx / R4, c4 = idx % R4;
-            const float4 v4 = *(const float4 *)(vb + (size_t)(base + r) * kv + 4 * c4);
-            const float pt = e[at(base + r)];
-            *(float4 *)(buf + r * HD + 4 * c4) = make_float4(pt * v4.x, pt * v4.y, pt * v4.z, pt * v4.w);
-        }
-        __syncthreads();
-        if (tid < HD) {
-            const float *bp = buf + tid;
-            int r = 0;
-            for (; r + 16 <= rows; r += 16) {
-                float v[16];
 #pragma unroll
-                for (int k = 0; k < 16; k++) v[k] = bp[(r + k) * HD];
+    for (int j = 0; j < PD; j++) issue(ring[j], j);
+    for (int c0 = 0; c0 < nch; c0 += PD) {
 #pragma unroll
-                for (int k = 0; k < 16; k++) o += v[k];
+        for (int j = 0; j < PD; j++) {
+            const int c = c0 + j;
+            if (c < nch) {
+                float *buf = prod + (c & 1) * SV_BUF;
+                const int base = c * CP;
+                const int rows = min(CP, cnt - base);
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    const int idx = tid + k * SEQ_T;
+                    const int r = idx / R4;
+                    const float pt = r < rows ? e[at(base + r)] : 0.0f;
+                    const float4 v4 = ring[j][k];
+                    *(float4 *)(buf + idx * 4) = make_float4(pt * v4.x, pt * v4.y, pt * v4.z, pt * v4.w);
+                }
+                issue(ring[j], c + PD);
+                __syncthreads();
+                if (tid < DB) {
+                    const float *bp = buf + tid;
+                    int r = 0;
+                    for (; r + 16 <= rows; r += 16) {
+                        float v[16];
+#pragma unroll
+                        for (int k = 0; k < 16; k++) v[k] = bp[(r + k) * DB];
+#pragma unroll
+                        for (int k = 0; k < 16; k++) o += v[k];
+                    }
+                    for (; r < rows; r++) o += bp[r * DB];
+                }
             }
-            for (; r < rows; r++) o += bp[r * HD];
         }
     }
-    if (tid < HD) a.out[i * (size_t)a.n_head * HD + (size_t)h * HD + tid] = o;
+    ATT_TS(4);
+    if (tid < DB) a.out[i * (size_t)a.n_head * HD + (size_t)h * HD + d0 + tid] = o;
 }
 
 static void launch_sv(const AttnArgs &a, size_t head_dim, size_t m, hipStream_t s) {
-    dim3 g((unsigned)a.n_head, (unsigned)m);
+    dim3 g((unsigned)(a.n_head * (head_dim / SV_DB)), (unsigned)m);
     switch (head_dim) {
     case 64: k_attn_sv<64><<<g, SEQ_T, 0, s>>>(a); break;
     case 128: k_attn_sv<128><<<g, SEQ_T, 0, s>>>(a); break;

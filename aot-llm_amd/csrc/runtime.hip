@@ -10,6 +10,7 @@
 
 #include <string>
 #include <vector>
+#include <stdlib.h>
 
 #include "internal.hpp"
 
@@ -739,10 +740,15 @@ struct aotk_state {
     uint32_t *hist;    // [ctx]
     uint32_t *ctl_host;  // pinned staging for the control words
     std::vector<void *> allocs;
+    // One greedy generation step (argmax, advance, decode step, position
+    // increment) captured once as a HIP graph; every kernel of it reads the
+    // token and the position from `ctl`, so the same graph serves every step.
+    hipGraphExec_t gen_exec = nullptr;
 };
 
 static void state_release(aotk_state *st) {
     (void)hipStreamSynchronize(g_stream);
+    if (st->gen_exec) (void)hipGraphExecDestroy(st->gen_exec);
     for (void *p : st->allocs) (void)hipFree(p);
     if (st->ctl_host) (void)hipHostFree(st->ctl_host);
     delete st;
@@ -889,10 +895,10 @@ static void run_layers(aotk_state *st, size_t m, size_t pos0, const int *pos_dev
         // attention block
         launch_rmsnorm_quant(st->x, L.attn_norm, dim, m, d.eps, outs_for(st, {L.wq.kind, L.wk.kind, L.wv.kind}, st->xb), s);
         bool same = L.wq.kind == L.wk.kind && L.wk.kind == L.wv.kind && activation(L.wq.kind) != ACT_F32;
-        if (same && m == 1) {
+        if (same) {
             const DevWeight *ws[3] = {&L.wq, &L.wk, &L.wv};
             float *ys[3] = {st->q, st->k, st->v};
-            launch_matvec_multi(3, ws, ys, act_for(st, L.wq.kind, st->xb), s);
+            launch_matvec_multi(3, ws, ys, act_for(st, L.wq.kind, st->xb), m, s);
         } else {
             launch_matvec(L.wq, act_for(st, L.wq.kind, st->xb), m, st->q, nullptr, s);
             launch_matvec(L.wk, act_for(st, L.wk.kind, st->xb), m, st->k, nullptr, s);
@@ -934,10 +940,10 @@ static void run_layers(aotk_state *st, size_t m, size_t pos0, const int *pos_dev
         // feed-forward block
         launch_rmsnorm_quant(st->x, L.ffn_norm, dim, m, d.eps, outs_for(st, {L.gate.kind, L.up.kind}, st->xb), s);
         bool same2 = L.gate.kind == L.up.kind && activation(L.gate.kind) != ACT_F32;
-        if (same2 && m == 1) {
+        if (same2) {
             const DevWeight *ws[2] = {&L.gate, &L.up};
             float *ys[2] = {st->hb, st->hb2};
-            launch_matvec_multi(2, ws, ys, act_for(st, L.gate.kind, st->xb), s);
+            launch_matvec_multi(2, ws, ys, act_for(st, L.gate.kind, st->xb), m, s);
         } else {
             launch_matvec(L.gate, act_for(st, L.gate.kind, st->xb), m, st->hb, nullptr, s);
             launch_matvec(L.up, act_for(st, L.up.kind, st->xb), m, st->hb2, nullptr, s);
@@ -1026,14 +1032,30 @@ int aotk_generate_greedy(aotk_state *st, size_t pos, size_t n, uint32_t *tokens_
     st->ctl_host[3] = 0;
     HIPC(hipMemcpyAsync(st->ctl + 1, st->ctl_host + 1, 4, hipMemcpyHostToDevice, g_stream));
     HIPC(hipMemcpyAsync(st->ctl + 3, st->ctl_host + 3, 4, hipMemcpyHostToDevice, g_stream));
-    for (size_t g = 0; g < n; g++) {
+    auto step = [&]() {
         launch_argmax(st->logits, vocab, st->ctl + 2, st->am_ws, g_stream);
         launch_advance(st->ctl, (int *)(st->ctl + 3), st->hist, st->ctl + 2, g_stream);
-        if (g + 1 < n) {
-            run_decode_step(st, 1);
-            launch_inc((int *)(st->ctl + 1), g_stream);
+        run_decode_step(st, 1);
+        launch_inc((int *)(st->ctl + 1), g_stream);
+    };
+    if (n > 1 && !st->gen_exec && !getenv("AOTK_NO_GRAPH")) {
+        hipGraph_t graph = nullptr;
+        HIPC(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal));
+        step();
+        hipError_t e = hipStreamEndCapture(g_stream, &graph);
+        if (e == hipSuccess) e = hipGraphInstantiate(&st->gen_exec, graph, nullptr, nullptr, 0);
+        if (graph) (void)hipGraphDestroy(graph);
+        if (e != hipSuccess) {
+            st->gen_exec = nullptr;
+            return fail("graph capture of the decode step failed: %s", hipGetErrorString(e));
         }
     }
+    for (size_t g = 0; g + 1 < n; g++) {
+        if (st->gen_exec) HIPC(hipGraphLaunch(st->gen_exec, g_stream));
+        else step();
+    }
+    launch_argmax(st->logits, vocab, st->ctl + 2, st->am_ws, g_stream);
+    launch_advance(st->ctl, (int *)(st->ctl + 3), st->hist, st->ctl + 2, g_stream);
     HIPC(hipGetLastError());
     HIPC(hipMemcpyAsync(tokens_host, st->hist, n * 4, hipMemcpyDeviceToHost, g_stream));
     HIPC(hipStreamSynchronize(g_stream));

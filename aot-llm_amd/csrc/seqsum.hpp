@@ -57,6 +57,46 @@ struct SeqScratch {
     float result;
 };
 
+// Wave-wide inclusive scans with DPP row shifts and row broadcasts (GFX9
+// DPP: row_shr 1/2/4/8 within rows of 16 lanes, then row_bcast15 into rows
+// 1 and 3, row_bcast31 into rows 2 and 3). Lanes without a source read 0.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xf, true);
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double dpp_d(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = dpp_i<CTRL, ROWS>((int)(b & 0xffffffffLL)), hi = dpp_i<CTRL, ROWS>((int)(b >> 32));
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+__device__ __forceinline__ double wave_scan_d(double x) {
+    x += dpp_d<0x111, 0xf>(x);
+    x += dpp_d<0x112, 0xf>(x);
+    x += dpp_d<0x114, 0xf>(x);
+    x += dpp_d<0x118, 0xf>(x);
+    x += dpp_d<0x142, 0xa>(x);
+    x += dpp_d<0x143, 0xc>(x);
+    return x;
+}
+// Segmented (v, f) carry plus a plain count c, combined as
+// (v1,f1,c1) + (v2,f2,c2) = (f2 ? v2 : v1 + v2, f1 | f2, c1 + c2).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ void seg_step(int &v, int &f, int &c) {
+    const int ov = dpp_i<CTRL, ROWS>(v), of = dpp_i<CTRL, ROWS>(f), oc = dpp_i<CTRL, ROWS>(c);
+    v = f ? v : v + ov;
+    f |= of;
+    c += oc;
+}
+__device__ __forceinline__ void wave_scan_seg(int &v, int &f, int &c) {
+    seg_step<0x111, 0xf>(v, f, c);
+    seg_step<0x112, 0xf>(v, f, c);
+    seg_step<0x114, 0xf>(v, f, c);
+    seg_step<0x118, 0xf>(v, f, c);
+    seg_step<0x142, 0xa>(v, f, c);
+    seg_step<0x143, 0xc>(v, f, c);
+}
+
 __device__ __forceinline__ int dbl_exponent(double v) {  // floor(log2(v)) for normal v > 0
     return (int)((__double_as_longlong(v) >> 52) & 0x7ff) - 1023;
 }
@@ -138,12 +178,7 @@ __device__ __forceinline__ float exact_seq_sum_t(const float *pp, int n, SeqScra
     double loc = 0.0;
 #pragma unroll
     for (int i = 0; i < MAXC; i++) loc += (double)pr[i];
-    double incl = loc;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        double t = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += t;
-    }
+    const double incl = wave_scan_d(loc);
     if (lane == 63) S.wd[wave] = incl;
     __syncthreads();
     double P = incl - loc;
@@ -157,19 +192,29 @@ __device__ __forceinline__ float exact_seq_sum_t(const float *pp, int n, SeqScra
     const double delta = (double)(c1 + 2) * 0x1p-23;
     const double mlo = 1.0 - delta, mhi = 1.0 + delta;
     int ec[MAXC], g[MAXC];
+    // waves wholly past the end (short sums) skip the per-element work
+    const bool wave_busy = __builtin_amdgcn_readfirstlane(len > 0 ? 1 : 0) != 0;
+    if (wave_busy) {
 #pragma unroll
-    for (int i = 0; i < MAXC; i++) {
-        const float p = pr[i];
-        const double Pn = P + (double)p;
-        const int elo = dbl_exponent(P * mlo), ehi = dbl_exponent(Pn * mhi);
-        const int e = max(min(elo, 99), -89);
-        const float q = p * pow2f(23 - e);  // p / u, exact
-        const float fl = floorf(q);
-        const float fr = q - fl;
-        const bool ok = elo == ehi && elo == e && fr != 0.5f && fl < 16777216.0f;
-        ec[i] = ok ? e : SEQ_SINGLE;
-        g[i] = ok ? (int)fl + (fr > 0.5f ? 1 : 0) : 0;
-        P = Pn;
+        for (int i = 0; i < MAXC; i++) {
+            const float p = pr[i];
+            const double Pn = P + (double)p;
+            const int elo = dbl_exponent(P * mlo), ehi = dbl_exponent(Pn * mhi);
+            const int e = max(min(elo, 99), -89);
+            const float q = p * pow2f(23 - e);  // p / u, exact
+            const float fl = floorf(q);
+            const float fr = q - fl;
+            const bool ok = elo == ehi && elo == e && fr != 0.5f && fl < 16777216.0f;
+            ec[i] = ok ? e : SEQ_SINGLE;
+            g[i] = ok ? (int)fl + (fr > 0.5f ? 1 : 0) : 0;
+            P = Pn;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < MAXC; i++) {
+            ec[i] = SEQ_SINGLE;
+            g[i] = 0;
+        }
     }
     // run-local inclusive sums; the leading run of the chunk
     int lead = 0;  // elements of the leading run
@@ -209,15 +254,7 @@ __device__ __forceinline__ float exact_seq_sum_t(const float *pp, int n, SeqScra
         v = 0;
         f = 1;
     }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int ov = __shfl_up(v, o, 64), of = __shfl_up(f, o, 64), oc = __shfl_up(c, o, 64);
-        if (lane >= o) {
-            v = f ? v : v + ov;
-            f |= of;
-            c += oc;
-        }
-    }
+    wave_scan_seg(v, f, c);
     if (lane == 63) {
         S.wv[wave] = v;
         S.wf[wave] = f;
@@ -234,12 +271,7 @@ __device__ __forceinline__ float exact_seq_sum_t(const float *pp, int n, SeqScra
         total += S.wc[w];
     }
     {
-        int pv = __shfl_up(v, 1, 64), pf = __shfl_up(f, 1, 64), pc = __shfl_up(c, 1, 64);
-        if (lane == 0) {
-            pv = 0;
-            pf = 0;
-            pc = 0;
-        }
+        const int pv = dpp_i<0x138, 0xf>(v), pf = dpp_i<0x138, 0xf>(f), pc = dpp_i<0x138, 0xf>(c);  // wave_shr:1
         cv = pf ? pv : cv + pv;  // run value flowing into this chunk
         cc += pc;                // events ending before this chunk
     }
