@@ -136,6 +136,11 @@ void launch_matvec(const DevWeight &w, const void *x_act, size_t m, float *y, co
 // Up to three matrices sharing kind/cols/input in one launch (q/k/v, gate/up).
 void launch_matvec_multi(int n, const DevWeight *const ws[], float *const ys[], const void *x_act, size_t m,
                          hipStream_t s);
+// Matrices of a Q4_K/Q5_K kind (up to three, e.g. q and k) and one Q6_K
+// matrix (e.g. v) with <= 64 super-blocks per row, same input, one launch.
+bool matvec_pair_ok(const DevWeight &a, const DevWeight &b);
+void launch_matvec_pair(int na, const DevWeight *const wa[], float *const ya[], const DevWeight &wb, float *yb,
+                        const void *x_act, size_t m, hipStream_t s);
 
 // ops.hip
 struct RmsOut {

@@ -352,11 +352,9 @@ __device__ __forceinline__ float kq_term(const uint4 (&c)[KqGeom<KIND>::CH], flo
 // PF = 0: one row group per wave (G == 1), register budget for 4 waves per
 // SIMD; PF = 1: G groups per wave with the next group's loads in flight.
 template <int KIND, int PF>
-__global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq(MvArgs a, int RL, int G) {
+__device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int bx, uint8_t *sY, float (*sT)[256 + 16]) {
     using Geo = KqGeom<KIND>;
     constexpr int CH = Geo::CH;
-    __shared__ __align__(16) uint8_t sY[64 * KQ_REC];
-    __shared__ __align__(16) float sT[4][256 + 16];  // [wave][row slot * ts + super-block] (+ read slack)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tok = blockIdx.y;
     const int nb = a.nb;
@@ -365,7 +363,7 @@ __global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq(MvArgs a, int RL, int
     const int sa = lane_on ? s : 0;
     const size_t cs = (size_t)nb * 16;
     const size_t rowb = (size_t)nb * Geo::RB;
-    const int group0 = (blockIdx.x * 4 + wave) * G;
+    const int group0 = (bx * 4 + wave) * G;
     const int ts = (nb + 3) & ~3;  // row stride of the fold buffer (RL * ts <= 256)
 
     uint4 cur[CH], nxt[PF ? CH : 1];
@@ -435,6 +433,28 @@ __global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq(MvArgs a, int RL, int
             dcur = dnxt;
         }
     }
+}
+
+// LDS of one K-quant block: the activation records and the fold buffer.
+struct KqShared {
+    __align__(16) uint8_t y[64 * KQ_REC];
+    __align__(16) float t[4][256 + 16];  // [wave][row slot * ts + super-block] (+ read slack)
+};
+
+template <int KIND, int PF>
+__global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq(MvArgs a, int RL, int G) {
+    __shared__ KqShared sh;
+    mv_kq_body<KIND, PF>(a, RL, G, blockIdx.x, sh.y, sh.t);
+}
+
+// Two K-quant matrices of different kinds sharing the input in one launch
+// (q/k in one kind and v in another): blocks [0, nblk_a) run `a`, the rest
+// run `b`.
+template <int KA, int KB>
+__global__ __launch_bounds__(256, 2) void k_mv_kq2(MvArgs a, int RLa, int Ga, MvArgs b, int RLb, int Gb, int nblk_a) {
+    __shared__ KqShared sh;
+    if ((int)blockIdx.x < nblk_a) mv_kq_body<KA, 1>(a, RLa, Ga, blockIdx.x, sh.y, sh.t);
+    else mv_kq_body<KB, 1>(b, RLb, Gb, blockIdx.x - nblk_a, sh.y, sh.t);
 }
 
 // ------------------------------------------------------ Q8_0 / Q4_0 / Q5_0
@@ -598,17 +618,24 @@ static MvArgs make_args(int n, const DevWeight *const ws[], float *const ys[], c
     return a;
 }
 
+// Row slots per wave (RL), row groups per wave (G) and blocks of the
+// K-quant kernel: all waves resident in one round (3 waves per SIMD on 256
+// CUs), each doing G row groups.
+static void kq_shape(const MvArgs &a, int &RL, int &G, int &blocks) {
+    RL = 1;
+    while (RL * 2 * a.nb <= 64) RL *= 2;
+    const int groups = (a.total_rows + RL - 1) / RL;
+    G = (groups + 3071) / 3072;
+    G = G > 8 ? 8 : G;
+    blocks = (groups + 4 * G - 1) / (4 * G);
+}
+
 template <int KIND>
 static void launch_kq(const MvArgs &a, dim3 grid, hipStream_t s) {
     if (a.nb <= 64) {
-        int RL = 1;
-        while (RL * 2 * a.nb <= 64) RL *= 2;
-        // all waves resident in one round (3 waves per SIMD on 256 CUs),
-        // each doing G row groups
-        const int groups = (a.total_rows + RL - 1) / RL;
-        int G = (groups + 3071) / 3072;
-        G = G > 8 ? 8 : G;
-        grid.x = (unsigned)((groups + 4 * G - 1) / (4 * G));
+        int RL, G, blocks;
+        kq_shape(a, RL, G, blocks);
+        grid.x = (unsigned)blocks;
         k_mv_kq<KIND, 1><<<grid, 256, 0, s>>>(a, RL, G);
     } else {
         grid.x = (unsigned)((a.total_rows + 7) / 8);
@@ -668,6 +695,26 @@ void launch_matvec_multi(int n, const DevWeight *const ws[], float *const ys[], 
                          hipStream_t s) {
     MvArgs a = make_args(n, ws, ys, nullptr, x_act);
     launch_args(ws[0]->kind, a, m, s);
+}
+
+bool matvec_pair_ok(const DevWeight &a, const DevWeight &b) {
+    return ((a.kind == AOTK_Q4_K || a.kind == AOTK_Q5_K) && b.kind == AOTK_Q6_K) && a.cols == b.cols && a.nb <= 64;
+}
+
+void launch_matvec_pair(int na, const DevWeight *const wa[], float *const ya[], const DevWeight &wb, float *yb,
+                        const void *x_act, size_t m, hipStream_t s) {
+    MvArgs a = make_args(na, wa, ya, nullptr, x_act);
+    const DevWeight *wbs[1] = {&wb};
+    float *ybs[1] = {yb};
+    MvArgs b = make_args(1, wbs, ybs, nullptr, x_act);
+    int RLa, Ga, na_blk, RLb, Gb, nb_blk;
+    kq_shape(a, RLa, Ga, na_blk);
+    kq_shape(b, RLb, Gb, nb_blk);
+    dim3 grid((unsigned)(na_blk + nb_blk), (unsigned)m);
+    if (wa[0]->kind == AOTK_Q4_K)
+        k_mv_kq2<AOTK_Q4_K, AOTK_Q6_K><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk);
+    else
+        k_mv_kq2<AOTK_Q5_K, AOTK_Q6_K><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk);
 }
 
 }  // namespace aotk

@@ -899,6 +899,10 @@ static void run_layers(aotk_state *st, size_t m, size_t pos0, const int *pos_dev
             const DevWeight *ws[3] = {&L.wq, &L.wk, &L.wv};
             float *ys[3] = {st->q, st->k, st->v};
             launch_matvec_multi(3, ws, ys, act_for(st, L.wq.kind, st->xb), m, s);
+        } else if (L.wq.kind == L.wk.kind && matvec_pair_ok(L.wq, L.wv)) {
+            const DevWeight *ws[2] = {&L.wq, &L.wk};
+            float *ys[2] = {st->q, st->k};
+            launch_matvec_pair(2, ws, ys, L.wv, st->v, act_for(st, L.wq.kind, st->xb), m, s);
         } else {
             launch_matvec(L.wq, act_for(st, L.wq.kind, st->xb), m, st->q, nullptr, s);
             launch_matvec(L.wk, act_for(st, L.wk.kind, st->xb), m, st->k, nullptr, s);

@@ -34,14 +34,15 @@
 namespace aotk {
 
 constexpr int SEQ_MAX_N = 8192;
-// Inputs live in LDS in a padded chunk layout: with SEQ_T = 1024 threads,
-// thread t owns elements [t*C, t*C+C) (C = ceil(n/1024)) stored at
-// t*(C+1) + i, so the lanes of a wave walking their chunks spread over the
-// banks.
+// The sum runs in blocks of SEQ_T threads, of which the first seq_threads(n)
+// do the work (fewer threads carry less fixed per-thread work for short
+// sums). Inputs live in LDS in a padded chunk layout: working thread t owns
+// elements [t*C, t*C+C) (C = seq_chunk(n)) stored at t*(C+1) + i, so the
+// lanes of a wave walking their chunks spread over the banks.
 constexpr int SEQ_T = 1024;
-constexpr int SEQ_MAXC = SEQ_MAX_N / SEQ_T;
 constexpr int SEQ_PAD_N = SEQ_MAX_N + SEQ_T + 32;
-__device__ __forceinline__ int seq_chunk(int n) { return (n + SEQ_T - 1) / SEQ_T; }
+__device__ __forceinline__ int seq_threads(int n) { return n <= 1024 ? 256 : SEQ_T; }
+__device__ __forceinline__ int seq_chunk(int n) { return (n + seq_threads(n) - 1) / seq_threads(n); }
 __device__ __forceinline__ int seq_idx(int k, int C) { return (k / C) * (C + 1) + (k % C); }
 constexpr int SEQ_MAX_EV = 2048;
 constexpr int SEQ_SINGLE = -32768;  // binade code of an element added alone
@@ -160,125 +161,157 @@ __device__ __forceinline__ float seq_walk(const float *pp, int C, int total, con
 }
 
 // Exact sequential sum of p[0..n) (LDS, padded layout of seq_idx, all
-// p >= 0, 1 <= n <= SEQ_MAX_N, ceil(n / SEQ_T) <= MAXC). All SEQ_T threads
-// of the block call it after p is complete; all get the result.
-template <int MAXC>
+// p >= 0, 1 <= n <= SEQ_MAX_N). The first T threads work (T == seq_threads(n),
+// seq_chunk(n) <= MAXC); all SEQ_T threads of the block call it after p is
+// complete, and all get the result.
+template <int MAXC, int T>
 __device__ __forceinline__ float exact_seq_sum_t(const float *pp, int n, SeqScratch &S) {
-    constexpr int NW = SEQ_T / 64;
+    constexpr int NW = T / 64;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int C = seq_chunk(n);
-    const int c0 = min(tid * C, n), c1 = min(c0 + C, n);
+    const bool act = tid < T;  // wave-uniform; idle waves only meet the barriers
+    const int c0 = act ? min(tid * C, n) : n, c1 = min(c0 + C, n);
     const int len = c1 - c0;
     const int base = tid * (C + 1);
     SEQ_TS(0);
     // 1. double prefix sums
     float pr[MAXC];
+    double loc = 0.0, P = 0.0;
+    if (act) {
 #pragma unroll
-    for (int i = 0; i < MAXC; i++) pr[i] = i < len ? pp[base + i] : 0.0f;
-    double loc = 0.0;
+        for (int i = 0; i < MAXC; i++) pr[i] = i < len ? pp[base + i] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < MAXC; i++) loc += (double)pr[i];
-    const double incl = wave_scan_d(loc);
-    if (lane == 63) S.wd[wave] = incl;
+        for (int i = 0; i < MAXC; i++) loc += (double)pr[i];
+        const double incl = wave_scan_d(loc);
+        if (lane == 63) S.wd[wave] = incl;
+        P = incl - loc;
+    }
     __syncthreads();
-    double P = incl - loc;
+    if (act) {
 #pragma unroll
-    for (int w = 0; w < NW - 1; w++)
-        if (w < wave) P += S.wd[w];
+        for (int w = 0; w < NW - 1; w++)
+            if (w < wave) P += S.wd[w];
+    }
     SEQ_TS(1);
     // 2. classify: binade code and rounded increment of each element. The
     //    margin (c1 + 2) * 2^-23 bounds the drift of every partial sum of
     //    the chunk.
-    const double delta = (double)(c1 + 2) * 0x1p-23;
-    const double mlo = 1.0 - delta, mhi = 1.0 + delta;
     int ec[MAXC], g[MAXC];
+#pragma unroll
+    for (int i = 0; i < MAXC; i++) {
+        ec[i] = SEQ_SINGLE;
+        g[i] = 0;
+    }
+    int lead = 0, last_e = SEQ_SINGLE, last_g = 0;
     // waves wholly past the end (short sums) skip the per-element work
     const bool wave_busy = __builtin_amdgcn_readfirstlane(len > 0 ? 1 : 0) != 0;
     if (wave_busy) {
+        const double delta = (double)(c1 + 2) * 0x1p-23;
+        const double mlo = 1.0 - delta, mhi = 1.0 + delta;
+        // a chunk whose whole predicted range lies in one binade needs no
+        // per-element binade checks
+        const int ce_lo = dbl_exponent(P * mlo), ce_hi = dbl_exponent((P + loc) * mhi);
+        const bool chunk_one = len > 0 && ce_lo == ce_hi && ce_lo > -89 && ce_lo < 99;
+        if (chunk_one) {
+            const float scale = pow2f(23 - ce_lo);
+#pragma unroll
+            for (int i = 0; i < MAXC; i++) {
+                const float q = pr[i] * scale;  // p / u, exact
+                const float fl = floorf(q);
+                const float fr = q - fl;
+                const bool ok = fr != 0.5f && fl < 16777216.0f;
+                ec[i] = ok ? ce_lo : SEQ_SINGLE;
+                g[i] = ok ? (int)fl + (fr > 0.5f ? 1 : 0) : 0;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < MAXC; i++) {
+                const float p = pr[i];
+                const double Pn = P + (double)p;
+                const int elo = dbl_exponent(P * mlo), ehi = dbl_exponent(Pn * mhi);
+                const int e = max(min(elo, 99), -89);
+                const float q = p * pow2f(23 - e);  // p / u, exact
+                const float fl = floorf(q);
+                const float fr = q - fl;
+                const bool ok = elo == ehi && elo == e && fr != 0.5f && fl < 16777216.0f;
+                ec[i] = ok ? e : SEQ_SINGLE;
+                g[i] = ok ? (int)fl + (fr > 0.5f ? 1 : 0) : 0;
+                P = Pn;
+            }
+        }
+        // run-local inclusive sums; the leading run of the chunk
+        bool in_lead = ec[0] != SEQ_SINGLE;
 #pragma unroll
         for (int i = 0; i < MAXC; i++) {
-            const float p = pr[i];
-            const double Pn = P + (double)p;
-            const int elo = dbl_exponent(P * mlo), ehi = dbl_exponent(Pn * mhi);
-            const int e = max(min(elo, 99), -89);
-            const float q = p * pow2f(23 - e);  // p / u, exact
-            const float fl = floorf(q);
-            const float fr = q - fl;
-            const bool ok = elo == ehi && elo == e && fr != 0.5f && fl < 16777216.0f;
-            ec[i] = ok ? e : SEQ_SINGLE;
-            g[i] = ok ? (int)fl + (fr > 0.5f ? 1 : 0) : 0;
-            P = Pn;
+            if (i > 0) {
+                const bool same = ec[i] != SEQ_SINGLE && ec[i] == ec[i - 1];
+                g[i] = same ? g[i] + g[i - 1] : g[i];
+                in_lead = in_lead && same;
+            }
+            lead += (in_lead && i < len) ? 1 : 0;
         }
-    } else {
+#pragma unroll
+        for (int i = 0; i < MAXC; i++)
+            if (i == len - 1) {
+                last_e = ec[i];
+                last_g = g[i];
+            }
+    }
+    if (act) {
+        S.e_first[tid] = len > 0 ? ec[0] : SEQ_SINGLE;
+        S.e_last[tid] = len > 0 ? last_e : SEQ_SINGLE;
+    }
+    __syncthreads();
+    int cv = 0, cc = 0, total = 0, after_e = SEQ_SINGLE;
+    bool cont = false;
+    int v = 0, f = 1, c = 0;
+    if (act) {
+        const int before_e = tid > 0 ? S.e_last[tid - 1] : SEQ_SINGLE;
+        after_e = (c1 < n && tid + 1 < T) ? S.e_first[tid + 1] : SEQ_SINGLE;
+        cont = len > 0 && ec[0] != SEQ_SINGLE && ec[0] == before_e;
+        // events ending in this chunk
+        int n_end = 0;
 #pragma unroll
         for (int i = 0; i < MAXC; i++) {
-            ec[i] = SEQ_SINGLE;
-            g[i] = 0;
+            const int next = i + 1 < len ? ec[i + 1 < MAXC ? i + 1 : i] : after_e;
+            n_end += (i < len && (ec[i] == SEQ_SINGLE || next != ec[i])) ? 1 : 0;
         }
-    }
-    // run-local inclusive sums; the leading run of the chunk
-    int lead = 0;  // elements of the leading run
-    bool in_lead = ec[0] != SEQ_SINGLE;
-#pragma unroll
-    for (int i = 0; i < MAXC; i++) {
-        if (i > 0) {
-            const bool same = ec[i] != SEQ_SINGLE && ec[i] == ec[i - 1];
-            g[i] = same ? g[i] + g[i - 1] : g[i];
-            in_lead = in_lead && same;
+        // block scans: segmented run carry (v, f) and event offsets (c)
+        v = last_g;
+        f = (cont && lead == len) ? 0 : 1;
+        c = n_end;
+        if (len == 0) {
+            v = 0;
+            f = 1;
         }
-        lead += (in_lead && i < len) ? 1 : 0;
-    }
-    int last_e = SEQ_SINGLE, last_g = 0;
-#pragma unroll
-    for (int i = 0; i < MAXC; i++)
-        if (i == len - 1) {
-            last_e = ec[i];
-            last_g = g[i];
+        wave_scan_seg(v, f, c);
+        if (lane == 63) {
+            S.wv[wave] = v;
+            S.wf[wave] = f;
+            S.wc[wave] = c;
         }
-    S.e_first[tid] = len > 0 ? ec[0] : SEQ_SINGLE;
-    S.e_last[tid] = len > 0 ? last_e : SEQ_SINGLE;
-    __syncthreads();
-    const int before_e = tid > 0 ? S.e_last[tid - 1] : SEQ_SINGLE;
-    const int after_e = (c1 < n && tid + 1 < SEQ_T) ? S.e_first[tid + 1] : SEQ_SINGLE;
-    const bool cont = len > 0 && ec[0] != SEQ_SINGLE && ec[0] == before_e;
-    // events ending in this chunk
-    int n_end = 0;
-#pragma unroll
-    for (int i = 0; i < MAXC; i++) {
-        const int next = i + 1 < len ? ec[i + 1 < MAXC ? i + 1 : i] : after_e;
-        n_end += (i < len && (ec[i] == SEQ_SINGLE || next != ec[i])) ? 1 : 0;
-    }
-    // block scans: segmented run carry (v, f) and event offsets (c)
-    int v = last_g, f = (cont && lead == len) ? 0 : 1, c = n_end;
-    if (len == 0) {
-        v = 0;
-        f = 1;
-    }
-    wave_scan_seg(v, f, c);
-    if (lane == 63) {
-        S.wv[wave] = v;
-        S.wf[wave] = f;
-        S.wc[wave] = c;
     }
     __syncthreads();
-    int cv = 0, cc = 0, total = 0;
+    if (act) {
 #pragma unroll
-    for (int w = 0; w < NW; w++) {
-        if (w < wave) {
-            cv = S.wf[w] ? S.wv[w] : cv + S.wv[w];
-            cc += S.wc[w];
+        for (int w = 0; w < NW; w++) {
+            if (w < wave) {
+                cv = S.wf[w] ? S.wv[w] : cv + S.wv[w];
+                cc += S.wc[w];
+            }
+            total += S.wc[w];
         }
-        total += S.wc[w];
-    }
-    {
         const int pv = dpp_i<0x138, 0xf>(v), pf = dpp_i<0x138, 0xf>(f), pc = dpp_i<0x138, 0xf>(c);  // wave_shr:1
         cv = pf ? pv : cv + pv;  // run value flowing into this chunk
         cc += pc;                // events ending before this chunk
+    } else {
+#pragma unroll
+        for (int w = 0; w < NW; w++) total += S.wc[w];
     }
     SEQ_TS(2);
     // 3. write the events at their slots
     const bool fits = total <= SEQ_MAX_EV;
-    if (fits) {
+    if (fits && act) {
         int slot = cc;
 #pragma unroll
         for (int i = 0; i < MAXC; i++) {
@@ -309,9 +342,9 @@ __device__ __forceinline__ float exact_seq_sum_t(const float *pp, int n, SeqScra
 
 __device__ __forceinline__ float exact_seq_sum(const float *pp, int n, SeqScratch &S) {
     const int C = seq_chunk(n);
-    if (C <= 2) return exact_seq_sum_t<2>(pp, n, S);
-    if (C <= 4) return exact_seq_sum_t<4>(pp, n, S);
-    return exact_seq_sum_t<SEQ_MAXC>(pp, n, S);
+    if (seq_threads(n) == 256) return exact_seq_sum_t<4, 256>(pp, n, S);
+    if (C <= 4) return exact_seq_sum_t<4, SEQ_T>(pp, n, S);
+    return exact_seq_sum_t<SEQ_MAX_N / SEQ_T, SEQ_T>(pp, n, S);
 }
 
 }  // namespace aotk
