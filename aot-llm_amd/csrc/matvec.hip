@@ -314,9 +314,10 @@ __device__ __forceinline__ float kq_term(const uint4 (&c)[KqGeom<KIND>::CH], flo
             int sc0, m0, sc1, m1;
             scale_min_k4(2 * jp, hdr.y, hdr.z, hdr.w, sc0, m0);
             scale_min_k4(2 * jp + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
-            sumi += sc0 * slo + sc1 * shi;
-            summ += m0 * (bs(4 * jp) + bs(4 * jp + 1)) + m1 * (bs(4 * jp + 2) + bs(4 * jp + 3));
-            __builtin_amdgcn_sched_barrier(0);  // bound the live activation registers
+            // 24-bit multiplies (full rate): every factor fits in 24 bits
+            sumi += __mul24(sc0, slo) + __mul24(sc1, shi);
+            summ += __mul24(m0, bs(4 * jp) + bs(4 * jp + 1)) + __mul24(m1, bs(4 * jp + 2) + bs(4 * jp + 3));
+            asm volatile("" ::: "memory");  // keep the activation reads local
         }
         const float dd = f16_to_f32(hdr.x & 0xFFFFu) * yd;
         const float dm = f16_to_f32(hdr.x >> 16) * yd;
@@ -341,8 +342,8 @@ __device__ __forceinline__ float kq_term(const uint4 (&c)[KqGeom<KIND>::CH], flo
                 sg = dot4(v, yw[k], sg);
             }
             const int sc = (int)(int8_t)((scw[g >> 2] >> (8 * (g & 3))) & 0xFFu);
-            sumi += sc * (sg - 32 * bs(g));
-            if ((g & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+            sumi += __mul24(sc, sg - 32 * bs(g));  // |sg - 32 bs| < 2^18
+            if ((g & 3) == 3) asm volatile("" ::: "memory");  // keep the activation reads local
         }
         const float dd = d6 * yd;
         return dd * (float)sumi;
@@ -395,17 +396,15 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
     MV_TS(1);
     const uint8_t *rec = sY + sa * KQ_REC;
     const int ng = PF ? G : 1;
-    for (int gi = 0; gi < ng; gi++) {
+    // one row group: the term, the fold in super-block order (terms read 16
+    // at a time ahead of the dependent adds), the store
+    auto group = [&](const uint4 *c, float d6, int gi) {
         const int gr0 = (group0 + gi) * RL;
-        if (gr0 >= a.total_rows) break;
-        if (PF && gi + 1 < G) load(nxt, dnxt, gi + 1);
-        const float term = kq_term<KIND>(cur, dcur, rec);
+        const float term = kq_term<KIND>(*(const uint4(*)[CH])c, d6, rec);
         MV_TS(2 + 2 * gi);
         if (lane_on) sT[wave][rs * ts + s] = term;
         wave_lds_sync();
         if (lane < RL && gr0 + lane < a.total_rows) {
-            // fold in super-block order; the terms are read 16 at a time
-            // ahead of the dependent adds
             const float4 *tp = (const float4 *)&sT[wave][lane * ts];
             float acc = 0.0f;
             for (int k0 = 0; k0 < nb; k0 += 16) {
@@ -427,11 +426,15 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
         }
         wave_lds_sync();
         MV_TS(3 + 2 * gi);
-        if (PF && gi + 1 < G) {
-#pragma unroll
-            for (int k = 0; k < CH; k++) cur[k] = nxt[PF ? k : 0];
-            dcur = dnxt;
-        }
+    };
+    // groups alternate between the two register buffers (no copies)
+    for (int gi = 0; gi < ng; gi += 2) {
+        if ((group0 + gi) * RL >= a.total_rows) break;
+        if (PF && gi + 1 < ng) load(nxt, dnxt, gi + 1);
+        group(cur, dcur, gi);
+        if (!PF || gi + 1 >= ng || (group0 + gi + 1) * RL >= a.total_rows) break;
+        if (gi + 2 < ng) load(cur, dcur, gi + 2);
+        group(nxt, dnxt, gi + 1);
     }
 }
 
