@@ -460,6 +460,214 @@ __global__ __launch_bounds__(256, 2) void k_mv_kq2(MvArgs a, int RLa, int Ga, Mv
     else mv_kq_body<KB, 1>(b, RLb, Gb, blockIdx.x - nblk_a, sh.y, sh.t);
 }
 
+// ------------------------------------------------- K-quant matmul (MFMA)
+// Prompt batches (m tokens, 2 <= m <= 64): block = 16 weight rows x 64
+// tokens, wave w taking the 16-token tile w. Per super-block, v_mfma_i32_16x16x32_i8 computes exact
+// integer dot products of 32 values: A = activations (16 tokens x 32 k),
+// B = the quants of the wave's 16 rows (32 k x 16 rows), so lane l owns
+// weight row l % 16 and tokens 4*(l/16) + i of each 16-token tile. Per
+// sub-block the integer sums are scaled by the lane's row scale (exact
+// integer arithmetic) and, for Q4_K/Q5_K, summ = sum m_j * y is accumulated by
+// a second MFMA with the mins broadcast. The f32 fold per super-block is the
+// same expression, in the same order, as the matvec (bit-identical to m
+// matvecs, matvec.rs:479-583). Activations are staged per super-block in LDS
+// (double-buffered), the next super-block's quants are loaded ahead.
+typedef int mm_v4i __attribute__((ext_vector_type(4)));
+constexpr int MM_TOK = 64;        // tokens per block (4 tiles of 16)
+constexpr int MM_MIN_TOKENS = 2;  // smaller batches use the matvec kernels
+constexpr int MM_YS = 256 + 8;    // LDS bytes per token row of one super-block (padded)
+
+template <int KIND>
+struct MmW {
+    uint4 hdr;      // Q4_K/Q5_K: d, dmin, scales; Q6_K: the 16 scales
+    uint2 q[4];     // Q4_K/Q5_K: qs bytes for sub-block pairs; Q6_K: ql bytes for j = 0..3 ...
+    uint2 q2[4];    // Q5_K: qh bytes (pairs); Q6_K: ql bytes for j = 4..7
+    uint2 h6[8];    // Q6_K: qh bytes per j
+    float d6;
+};
+
+// Load the lane's share of super-block sb of row `row`: for each 32-value
+// step j, the 8 values k = 32j + 8q .. +8 (q = lane / 16).
+template <int KIND>
+__device__ __forceinline__ void mm_load(MmW<KIND> &w, const uint8_t *rowp, const uint16_t *drow, int sb, int nb, int q) {
+    const size_t cs = (size_t)nb * 16;
+    const uint8_t *b = rowp + (size_t)sb * 16;
+    if (KIND == AOTK_Q4_K || KIND == AOTK_Q5_K) {
+        constexpr int QC = KIND == AOTK_Q4_K ? 1 : 3;
+        w.hdr = *(const uint4 *)b;
+        // pair p (sub-blocks 2p, 2p+1): qs bytes 32p + 8q .. +8 -> chunk QC + 2p + q/2, offset 8*(q%2)
+#pragma unroll
+        for (int p = 0; p < 4; p++) w.q[p] = *(const uint2 *)(b + (QC + 2 * p + (q >> 1)) * cs + 8 * (q & 1));
+        if (KIND == AOTK_Q5_K)  // qh bytes 8q .. +8 -> chunk 1 + q/2
+#pragma unroll
+            for (int p = 0; p < 4; p++) w.q2[p] = *(const uint2 *)(b + (1 + (q >> 1)) * cs + 8 * (q & 1));
+    } else {
+        w.hdr = *(const uint4 *)(b + 12 * cs);
+        w.d6 = f16_to_f32(drow[sb]);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            // k0 = 32j + 8q: half n = j/4, quarter = j%4, l = 8q
+            const int n = j >> 2, quarter = j & 3;
+            const int qlo = 64 * n + 8 * q + 32 * (quarter & 1);  // ql byte offset
+            const int qho = 128 + 32 * n + 8 * q;                  // qh byte offset
+            const uint2 lo = *(const uint2 *)(b + (qlo >> 4) * cs + (qlo & 15));
+            if (j < 4) w.q[j] = lo;
+            else w.q2[j - 4] = lo;
+            w.h6[j] = *(const uint2 *)(b + (qho >> 4) * cs + (qho & 15));
+        }
+    }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void k_mm_kq(MvArgs a, int m) {
+    __shared__ __align__(16) uint8_t sY[2][MM_TOK * MM_YS];
+    __shared__ float sD[2][MM_TOK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int q = lane >> 4, r16 = lane & 15;
+    const int nb = a.nb;
+    const int grow = blockIdx.x * 16 + r16;  // this lane's weight row
+    const bool row_ok = grow < a.total_rows;
+    int local;
+    const int sg = seg_of(a, row_ok ? grow : 0, local);
+    const size_t rowb = (size_t)nb * KqGeom<KIND>::RB;
+    const uint8_t *rowp = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * rowb;
+    const uint16_t *drow = KIND == AOTK_Q6_K ? (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb : nullptr;
+    const int t = wave;                       // this wave's token tile
+    const bool tile_on = 16 * t < m;
+
+    // activation staging: tokens x 256 bytes + d of super-block sb
+    uint4 stg[4];
+    float stgd = 0.0f;
+    auto stage_load = [&](int sb) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int idx = tid + 256 * k;  // 64 tokens x 16 uint4
+            const int t = idx >> 4, c = idx & 15;
+            stg[k] = t < m ? *(const uint4 *)(a.xq + (size_t)t * a.cols + (size_t)sb * 256 + 16 * c) : make_uint4(0, 0, 0, 0);
+        }
+        if (tid < MM_TOK) stgd = tid < m ? a.xd[(size_t)tid * nb + sb] : 0.0f;
+    };
+    auto stage_store = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int idx = tid + 256 * k;
+            const int t = idx >> 4, c = idx & 15;
+            *(uint4 *)(sY[buf] + t * MM_YS + 16 * c) = stg[k];
+        }
+        if (tid < MM_TOK) sD[buf][tid] = stgd;
+    };
+
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    MmW<KIND> cur, nxt;
+    mm_load<KIND>(cur, rowp, drow, 0, nb, q);
+    stage_load(0);
+    stage_store(0);
+    __syncthreads();
+    for (int sb = 0; sb < nb; sb++) {
+        const int buf = sb & 1;
+        const bool more = sb + 1 < nb;
+        if (more) {
+            mm_load<KIND>(nxt, rowp, drow, sb + 1, nb, q);
+            stage_load(sb + 1);
+        }
+        // the lane row's scales (and mins) of this super-block
+        int sc[16], mn[8];
+        if (KIND == AOTK_Q6_K) {
+            const uint32_t scw[4] = {cur.hdr.x, cur.hdr.y, cur.hdr.z, cur.hdr.w};
+#pragma unroll
+            for (int g = 0; g < 16; g++) sc[g] = (int)(int8_t)((scw[g >> 2] >> (8 * (g & 3))) & 0xFFu);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) scale_min_k4(j, cur.hdr.y, cur.hdr.z, cur.hdr.w, sc[j], mn[j]);
+        }
+        // B fragments (the lane's 8 values of each 32-value step j)
+        long bq[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            uint32_t w0, w1;
+            if (KIND == AOTK_Q6_K) {
+                const uint2 lo = j < 4 ? cur.q[j] : cur.q2[j - 4];
+                const int quarter = j & 3, sh = 2 * quarter;
+                const uint32_t n0 = quarter >= 2 ? (lo.x >> 4) & 0x0F0F0F0Fu : lo.x & 0x0F0F0F0Fu;
+                const uint32_t n1 = quarter >= 2 ? (lo.y >> 4) & 0x0F0F0F0Fu : lo.y & 0x0F0F0F0Fu;
+                const uint32_t v0 = n0 | (((cur.h6[j].x >> sh) & 0x03030303u) << 4);
+                const uint32_t v1 = n1 | (((cur.h6[j].y >> sh) & 0x03030303u) << 4);
+                // q - 32 per byte (values 0..63, no borrow between bytes)
+                w0 = (v0 | 0x80808080u) - 0x20202020u;
+                w0 ^= 0x80808080u;
+                w1 = (v1 | 0x80808080u) - 0x20202020u;
+                w1 ^= 0x80808080u;
+            } else {
+                const uint2 qb = cur.q[j >> 1];
+                const int hi = j & 1;
+                w0 = hi ? (qb.x >> 4) & 0x0F0F0F0Fu : qb.x & 0x0F0F0F0Fu;
+                w1 = hi ? (qb.y >> 4) & 0x0F0F0F0Fu : qb.y & 0x0F0F0F0Fu;
+                if (KIND == AOTK_Q5_K) {
+                    const uint2 hb = cur.q2[j >> 1];
+                    w0 |= ((hb.x >> j) & 0x01010101u) << 4;
+                    w1 |= ((hb.y >> j) & 0x01010101u) << 4;
+                }
+            }
+            bq[j] = (long)(((unsigned long)w1 << 32) | w0);
+        }
+        const uint8_t *ys = sY[buf];
+        if (tile_on) {
+            // A fragments: token 16t + r16, k = 32j + 8q .. +8
+            const uint8_t *yrow = ys + (16 * t + r16) * MM_YS + 8 * q;
+            int sumi[4] = {0, 0, 0, 0};
+            mm_v4i csum = {0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const long av = *(const long *)(yrow + 32 * j);
+                if (KIND == AOTK_Q6_K) {
+                    // two 16-value scale groups per step: lanes q < 2 hold group 2j, q >= 2 group 2j+1
+                    const long b_lo = q < 2 ? bq[j] : 0, b_hi = q < 2 ? 0 : bq[j];
+                    mm_v4i c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
+                    c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b_lo, c0, 0, 0, 0);
+                    c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b_hi, c1, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) sumi[i] += __mul24(sc[2 * j], c0[i]) + __mul24(sc[2 * j + 1], c1[i]);
+                } else {
+                    mm_v4i c = {0, 0, 0, 0};
+                    c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bq[j], c, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) sumi[i] += __mul24(sc[j], c[i]);
+                    const long mb = (long)(0x0101010101010101ULL * (unsigned long)mn[j]);
+                    csum = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, mb, csum, 0, 0, 0);
+                }
+            }
+            // fold: tokens 16t + 4q + i of the lane's row
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float yd = sD[buf][16 * t + 4 * q + i];
+                float term;
+                if (KIND == AOTK_Q6_K) {
+                    const float dd = cur.d6 * yd;
+                    term = dd * (float)sumi[i];
+                } else {
+                    const float dd = f16_to_f32(cur.hdr.x & 0xFFFFu) * yd;
+                    const float dm = f16_to_f32(cur.hdr.x >> 16) * yd;
+                    term = dd * (float)sumi[i] - dm * (float)csum[i];
+                }
+                acc[i] = acc[i] + term;
+            }
+        }
+        if (more) {
+            stage_store(buf ^ 1);
+            cur = nxt;
+        }
+        __syncthreads();
+    }
+    if (row_ok && tile_on) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int tok = 16 * t + 4 * q + i;
+            if (tok < m) store_row(a, grow, tok, acc[i]);
+        }
+    }
+}
+
 // ------------------------------------------------------ Q8_0 / Q4_0 / Q5_0
 // Wave = 8 rows. Phase A: lanes turn 32 blocks of 2 rows per pass into the 8
 // per-lane integer sums P and the scale D = f16(d) * y.d, staged in LDS.
@@ -649,6 +857,16 @@ static void launch_kq(const MvArgs &a, dim3 grid, hipStream_t s) {
 static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
     dim3 grid;
     grid.y = (unsigned)m;
+    if (m >= MM_MIN_TOKENS && m <= MM_TOK && (kind == AOTK_Q4_K || kind == AOTK_Q5_K || kind == AOTK_Q6_K) &&
+        !getenv("AOTK_NO_MFMA")) {
+        dim3 g((unsigned)((a.total_rows + 15) / 16), 1);
+        switch (kind) {
+        case AOTK_Q4_K: k_mm_kq<AOTK_Q4_K><<<g, 256, 0, s>>>(a, (int)m); break;
+        case AOTK_Q5_K: k_mm_kq<AOTK_Q5_K><<<g, 256, 0, s>>>(a, (int)m); break;
+        default: k_mm_kq<AOTK_Q6_K><<<g, 256, 0, s>>>(a, (int)m); break;
+        }
+        return;
+    }
     switch (kind) {
     case AOTK_Q4_K:
         launch_kq<AOTK_Q4_K>(a, grid, s);
@@ -706,6 +924,11 @@ bool matvec_pair_ok(const DevWeight &a, const DevWeight &b) {
 
 void launch_matvec_pair(int na, const DevWeight *const wa[], float *const ya[], const DevWeight &wb, float *yb,
                         const void *x_act, size_t m, hipStream_t s) {
+    if (m >= MM_MIN_TOKENS) {  // batches: the MFMA matmul per kind
+        launch_matvec_multi(na, wa, ya, x_act, m, s);
+        launch_matvec(wb, x_act, m, yb, nullptr, s);
+        return;
+    }
     MvArgs a = make_args(na, wa, ya, nullptr, x_act);
     const DevWeight *wbs[1] = {&wb};
     float *ybs[1] = {yb};
