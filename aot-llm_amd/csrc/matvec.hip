@@ -520,8 +520,8 @@ __device__ __forceinline__ void mm_load(MmW<KIND> &w, const uint8_t *rowp, const
 
 template <int KIND>
 __global__ __launch_bounds__(256) void k_mm_kq(MvArgs a, int m) {
-    __shared__ __align__(16) uint8_t sY[2][MM_TOK * MM_YS];
-    __shared__ float sD[2][MM_TOK];
+    __shared__ __align__(16) uint8_t sY[3][MM_TOK * MM_YS];
+    __shared__ float sD[3][MM_TOK];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int q = lane >> 4, r16 = lane & 15;
     const int nb = a.nb;
@@ -535,41 +535,48 @@ __global__ __launch_bounds__(256) void k_mm_kq(MvArgs a, int m) {
     const int t = wave;                       // this wave's token tile
     const bool tile_on = 16 * t < m;
 
-    // activation staging: tokens x 256 bytes + d of super-block sb
-    uint4 stg[4];
-    float stgd = 0.0f;
-    auto stage_load = [&](int sb) {
+    // activation staging: tokens x 256 bytes + d of super-block sb, two
+    // super-blocks ahead (register sets r0 / r1, LDS ring of 3)
+    struct Stg {
+        uint4 v[4];
+        float d;
+    };
+    auto stage_load = [&](Stg &r, int sb) {
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const int idx = tid + 256 * k;  // 64 tokens x 16 uint4
-            const int t = idx >> 4, c = idx & 15;
-            stg[k] = t < m ? *(const uint4 *)(a.xq + (size_t)t * a.cols + (size_t)sb * 256 + 16 * c) : make_uint4(0, 0, 0, 0);
+            const int tk = idx >> 4, c = idx & 15;
+            r.v[k] = tk < m ? *(const uint4 *)(a.xq + (size_t)tk * a.cols + (size_t)sb * 256 + 16 * c) : make_uint4(0, 0, 0, 0);
         }
-        if (tid < MM_TOK) stgd = tid < m ? a.xd[(size_t)tid * nb + sb] : 0.0f;
+        r.d = (tid < MM_TOK && tid < m) ? a.xd[(size_t)tid * nb + sb] : 0.0f;
     };
-    auto stage_store = [&](int buf) {
+    auto stage_store = [&](const Stg &r, int buf) {
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const int idx = tid + 256 * k;
-            const int t = idx >> 4, c = idx & 15;
-            *(uint4 *)(sY[buf] + t * MM_YS + 16 * c) = stg[k];
+            const int tk = idx >> 4, c = idx & 15;
+            *(uint4 *)(sY[buf] + tk * MM_YS + 16 * c) = r.v[k];
         }
-        if (tid < MM_TOK) sD[buf][tid] = stgd;
+        if (tid < MM_TOK) sD[buf][tid] = r.d;
     };
 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
-    MmW<KIND> cur, nxt;
+    MmW<KIND> cur, nxt, nx2;
+    Stg r0, r1;
     mm_load<KIND>(cur, rowp, drow, 0, nb, q);
-    stage_load(0);
-    stage_store(0);
+    stage_load(r0, 0);
+    stage_store(r0, 0);
+    if (nb > 1) {
+        mm_load<KIND>(nxt, rowp, drow, 1, nb, q);
+        stage_load(r1, 1);
+    }
     __syncthreads();
     for (int sb = 0; sb < nb; sb++) {
-        const int buf = sb & 1;
-        const bool more = sb + 1 < nb;
-        if (more) {
-            mm_load<KIND>(nxt, rowp, drow, sb + 1, nb, q);
-            stage_load(sb + 1);
+        const int buf = sb % 3;
+        if (sb + 2 < nb) {
+            mm_load<KIND>(nx2, rowp, drow, sb + 2, nb, q);
+            stage_load(r0, sb + 2);
         }
         // the lane row's scales (and mins) of this super-block
         int sc[16], mn[8];
@@ -653,11 +660,11 @@ __global__ __launch_bounds__(256) void k_mm_kq(MvArgs a, int m) {
                 acc[i] = acc[i] + term;
             }
         }
-        if (more) {
-            stage_store(buf ^ 1);
-            cur = nxt;
-        }
+        if (sb + 1 < nb) stage_store(r1, (sb + 1) % 3);
         __syncthreads();
+        cur = nxt;
+        nxt = nx2;
+        r1 = r0;
     }
     if (row_ok && tile_on) {
 #pragma unroll
