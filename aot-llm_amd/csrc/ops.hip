@@ -110,6 +110,13 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant(const float *__restrict
     const size_t m = blockIdx.x;
     const float *xr = x + m * n;
     const int C = seq_chunk(n);
+    // the norm weights are loaded before the sum (n <= 8 * blockDim.x)
+    float wv[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i = threadIdx.x + k * SEQ_T;
+        wv[k] = i < n ? w[i] : 0.0f;
+    }
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         float v = xr[i];
         row[i] = v;
@@ -118,10 +125,14 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant(const float *__restrict
     __syncthreads();
     float ss = exact_seq_sum(sq, n, S);
     float r = 1.0f / sqrtf(ss / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float v = row[i] * r * w[i];
-        row[i] = v;
-        if (out.f32) out.f32[m * n + i] = v;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i = threadIdx.x + k * SEQ_T;
+        if (i < n) {
+            const float v = row[i] * r * wv[k];
+            row[i] = v;
+            if (out.f32) out.f32[m * n + i] = v;
+        }
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
