@@ -142,6 +142,28 @@ def test_attention(aotk, oracle, hd, nh, nkv, window):
         assert np.array_equal(got, ref), (pos0, m, np.abs(got - ref).max())
 
 
+@pytest.mark.parametrize("hd,nh,nkv,window,ctx,cases", [
+    (128, 32, 8, 0, 4400, ((4300, 1), (2100, 2), (1500, 1))),
+    (256, 8, 4, 1024, 8300, ((8200, 1), (700, 3))),
+    (256, 8, 4, 0, 8300, ((8200, 1), (5000, 2))),
+])
+def test_attention_long_spans(aotk, oracle, hd, nh, nkv, window, ctx, cases):
+    """Spans past the one-thread softmax sum (exact parallel replay) and past
+    SEQ_MAX_N (sequential fallback)."""
+    rng = np.random.default_rng(hd + ctx)
+    kv = nkv * hd
+    kc = (rng.standard_normal(ctx * kv) * 0.5).astype(np.float32)
+    vc = rng.standard_normal(ctx * kv).astype(np.float32)
+    p = oracle.Pool(8)
+    for pos0, m in cases:
+        q = rng.standard_normal(m * nh * hd).astype(np.float32)
+        got = aotk.attention(q, kc, vc, nh, nkv, hd, ctx, 0, pos0, m, window)
+        ref = np.zeros(m * nh * hd, np.float32)
+        oracle.load().or_attention(p.p, oracle.ptr(ref), oracle.ptr(q), oracle.ptr(kc), oracle.ptr(vc), nh, nkv, hd, ctx,
+                                   0, pos0, m, window)
+        assert np.array_equal(got, ref), (pos0, m, np.abs(got - ref).max())
+
+
 def test_argmax(aotk, oracle):
     rng = np.random.default_rng(1)
     x = rng.standard_normal(128256).astype(np.float32)
