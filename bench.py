@@ -72,6 +72,35 @@ def time_kernel(aotk, kind, rows, cols, iters=200, min_bytes=1 << 30):
     return ms, copies
 
 
+def extra_config(aotk, configs, name, n_ctx, steps):
+    """Decode tok/s of another BASELINE config at its context: the KV cache
+    holds n_ctx positions (random values uploaded, standing in for the
+    prefill), then `steps` greedy forwards are timed."""
+    import numpy as np
+    spec = configs.build(name)
+    model = aotk.Model(spec, seed=SEED)
+    d = spec.d
+    st = aotk.State(model, n_ctx + steps + 2, 1)
+    kv = d["n_kv_head"] * d["head_dim"]
+    rng = np.random.default_rng(1)
+    k = (rng.standard_normal((d["n_layer"], n_ctx, kv)) * 0.5).astype(np.float32)
+    v = rng.standard_normal((d["n_layer"], n_ctx, kv)).astype(np.float32)
+    st.kv_upload(n_ctx, k, v)
+    del k, v
+    st.forward(1, n_ctx, True)
+    st.generate(n_ctx + 1, 4)  # warm-up (and graph capture)
+    aotk.sync()
+    t = time.perf_counter()
+    st.generate(n_ctx + 1, steps + 1)
+    aotk.sync()
+    dt = time.perf_counter() - t
+    wb = model.weight_bytes()
+    st.free()
+    model.free()
+    return dict(decode_tok_s=round(steps / dt, 2), context=n_ctx, steps=steps, weight_GB=round(wb / 1e9, 3),
+                note="KV cache of random values at the given context, then greedy decode")
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
     summary (FETCH_SIZE / WRITE_SIZE scaled by a copy kernel of known size),
@@ -140,6 +169,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-micro", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the Qwen3 / Gemma-3 decode lines")
     ap.add_argument("--micro-only", action="store_true",
                     help="only the Q4_K 14336x4096 matvec and a 256 MiB device copy (for rocprofv3 --pmc runs)")
     a = ap.parse_args()
@@ -202,6 +232,12 @@ def main():
                         kernel="k_mv_kq<Q4_K> 14336x4096 (ffn gate/up shape)",
                         bytes_per_launch=matvec_bytes(abi.Q4_K, 14336, 4096), us_per_launch=dom["us"])
 
+    extra = {}
+    if not a.no_extra:
+        for name, n_ctx in (("qwen3-8b-q8_0", 4096), ("gemma3-4b-q5km", 8192)):
+            extra[name] = extra_config(aotk, configs, name, n_ctx, 64)
+            log(f"{name}: {extra[name]['decode_tok_s']} tok/s decode at {n_ctx} context")
+
     cpu = None
     if not a.no_cpu:
         log("cpu baseline: downloading the weights and running the oracle ...")
@@ -230,6 +266,7 @@ def main():
         "decode_weight_bytes_per_token": wbytes,
         "decode_weight_GBs": round(wbytes * tok_s / 1e9, 1),
         "q4k_matvec": micro,
+        "other_configs": extra,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "greedy_head": gen[:8],
