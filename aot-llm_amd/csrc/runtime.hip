@@ -835,14 +835,19 @@ aotk_state *aotk_state_new(aotk_model *m, size_t ctx, size_t max_batch) {
     st->hist = (uint32_t *)alloc(ctx * 4);
     ok = ok && st->attn_ws && st->ctl && st->tokens && st->hist;
     if (ok && hipHostMalloc((void **)&st->ctl_host, 64, hipHostMallocDefault) != hipSuccess) ok = false;
+    // The tables are copied on the library stream, behind the zero fills
+    // queued there by alloc() (that stream does not synchronise with the
+    // null stream), and each host copy is waited for before it is refilled.
     std::vector<float> cs;
     rope_table(cs, ctx, d.rot_dim, d.rope_base, d.rope_scale, m->rope_freqs);
     st->cs = F(cs.size());
-    if (ok) ok = hipMemcpy(st->cs, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) == hipSuccess;
+    if (ok) ok = hipMemcpyAsync(st->cs, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, g_stream) == hipSuccess &&
+                 hipStreamSynchronize(g_stream) == hipSuccess;
     if (d.swa_window > 0) {
         rope_table(cs, ctx, d.rot_dim, d.rope_base_local, d.rope_scale_local, m->rope_freqs);
         st->cs_local = F(cs.size());
-        if (ok) ok = hipMemcpy(st->cs_local, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) == hipSuccess;
+        if (ok) ok = hipMemcpyAsync(st->cs_local, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, g_stream) == hipSuccess &&
+                     hipStreamSynchronize(g_stream) == hipSuccess;
     } else {
         st->cs_local = st->cs;
     }
