@@ -756,6 +756,143 @@ __global__ __launch_bounds__(256) void k_mv_q80(MvArgs a) {
     if (chain == 0 && grow < a.total_rows) store_row(a, grow, tok, v);
 }
 
+// Q8_0 / Q4_0 / Q5_0, inputs of up to Q8B_MAX_COLS: wave = Q8B_R rows; lane
+// = block index within a step of 64 blocks. Phase A: each lane forms, for
+// each of the wave's rows, the 8 per-lane integer sums P_l of its block and
+// the scale D = f16(d) * y.d (the activation is staged in LDS per block of
+// 256 threads), written to LDS; phase B: lane (row r, chain l) runs
+// acc_l = fma(D, P_l, acc_l) over the step's blocks in order. The next
+// step's weights are loaded during phase B. Then the avx2 horizontal sum.
+constexpr int Q8B_R = 4;
+constexpr int Q8B_MAX_COLS = 16384;
+constexpr int Q8B_PS = 64 * 9 + 8;  // floats per row in the P buffer (block stride 9, row pad 8)
+
+template <int KIND>
+struct Q8bW {
+    uint4 w0, w1;  // Q8_0: 32 quants; Q4_0/Q5_0: w0 = 16 nibble bytes
+    uint32_t qh;   // Q5_0
+    uint16_t d;
+};
+
+template <int KIND>
+__global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
+    constexpr int R = Q8B_R;
+    __shared__ __align__(16) int8_t sy[Q8B_MAX_COLS];
+    __shared__ float syd[Q8B_MAX_COLS / 32];
+    __shared__ float sP[4][R * Q8B_PS];
+    __shared__ float sD[4][R][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tok = blockIdx.y;
+    const int nb = a.nb;
+    // weights of this wave's rows (rows past the end read row 0)
+    const uint8_t *wq[R];
+    const uint16_t *wd[R];
+    const uint32_t *wh[R];
+    const int grow0 = (blockIdx.x * 4 + wave) * R;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        int local;
+        const int sg = seg_of(a, grow0 + r < a.total_rows ? grow0 + r : 0, local);
+        constexpr int QB = KIND == AOTK_Q8_0 ? 32 : 16;
+        wq[r] = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * nb * QB;
+        wd[r] = (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb;
+        wh[r] = KIND == AOTK_Q5_0 ? (const uint32_t *)seg_sel(sg, a.w2[0], a.w2[1], a.w2[2]) + (size_t)local * nb : nullptr;
+    }
+    auto load = [&](Q8bW<KIND> (&w)[R], int c0) {
+        const int b = min(c0 + lane, nb - 1);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            if (KIND == AOTK_Q8_0) {
+                w[r].w0 = *(const uint4 *)(wq[r] + (size_t)b * 32);
+                w[r].w1 = *(const uint4 *)(wq[r] + (size_t)b * 32 + 16);
+            } else {
+                w[r].w0 = *(const uint4 *)(wq[r] + (size_t)b * 16);
+                if (KIND == AOTK_Q5_0) w[r].qh = wh[r][b];
+            }
+            w[r].d = wd[r][b];
+        }
+    };
+    Q8bW<KIND> cur[R], nxt[R];
+    load(cur, 0);
+    {
+        const uint4 *xq = (const uint4 *)(a.xq + (size_t)tok * a.cols);
+        for (int i = tid; i < (int)(a.cols / 16); i += 256) ((uint4 *)sy)[i] = xq[i];
+        for (int i = tid; i < nb; i += 256) syd[i] = a.xd[(size_t)tok * nb + i];
+    }
+    __syncthreads();
+    const int rr = lane >> 3, chain = lane & 7;
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < nb; c0 += 64) {
+        if (c0 + 64 < nb) load(nxt, c0 + 64);
+        // phase A
+        const int b = c0 + lane;
+        if (b < nb) {
+            const uint4 y0 = *(const uint4 *)(sy + b * 32), y1 = *(const uint4 *)(sy + b * 32 + 16);
+            const uint32_t yw[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+            const float yd = syd[b];
+            int off[8];
+            if (KIND != AOTK_Q8_0)
+#pragma unroll
+                for (int l = 0; l < 8; l++) off[l] = dot4(KIND == AOTK_Q5_0 ? 0xF0F0F0F0u : 0xF8F8F8F8u, yw[l], 0);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                float P[8];
+                if (KIND == AOTK_Q8_0) {
+                    const uint32_t ww[8] = {cur[r].w0.x, cur[r].w0.y, cur[r].w0.z, cur[r].w0.w,
+                                            cur[r].w1.x, cur[r].w1.y, cur[r].w1.z, cur[r].w1.w};
+#pragma unroll
+                    for (int l = 0; l < 8; l++) P[l] = (float)dot4(ww[l], yw[l], 0);
+                } else {
+                    const uint32_t nw[4] = {cur[r].w0.x, cur[r].w0.y, cur[r].w0.z, cur[r].w0.w};
+#pragma unroll
+                    for (int l = 0; l < 8; l++) {
+                        uint32_t v = l < 4 ? (nw[l] & 0x0F0F0F0Fu) : ((nw[l - 4] >> 4) & 0x0F0F0F0Fu);
+                        if (KIND == AOTK_Q5_0) {
+                            const uint32_t b4 = (cur[r].qh >> (4 * l)) & 0xFu;
+                            const uint32_t spread = (b4 & 1u) | ((b4 & 2u) << 7) | ((b4 & 4u) << 14) | ((b4 & 8u) << 21);
+                            v |= spread << 4;
+                        }
+                        P[l] = (float)dot4(v, yw[l], off[l]);
+                    }
+                }
+                float *dst = &sP[wave][r * Q8B_PS + lane * 9];
+#pragma unroll
+                for (int l = 0; l < 8; l++) dst[l] = P[l];
+                sD[wave][r][lane] = f16_to_f32(cur[r].d) * yd;
+            }
+        }
+        wave_lds_sync();
+        // phase B: block order, one fma chain per (row, lane chain)
+        if (rr < R) {
+            const int n = nb - c0 < 64 ? nb - c0 : 64;
+            const float *pp = &sP[wave][rr * Q8B_PS + chain];
+            const float *dp = sD[wave][rr];
+            int i = 0;
+            for (; i + 8 <= n; i += 8) {
+                float pv[8], dv[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    pv[k] = pp[(i + k) * 9];
+                    dv[k] = dp[i + k];
+                }
+#pragma unroll
+                for (int k = 0; k < 8; k++) acc = fmaf(dv[k], pv[k], acc);
+            }
+            for (; i < n; i++) acc = fmaf(dp[i], pp[i * 9], acc);
+        }
+        wave_lds_sync();
+        if (c0 + 64 < nb)
+#pragma unroll
+            for (int r = 0; r < R; r++) cur[r] = nxt[r];
+    }
+    // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7))  (simd_avx2.rs:27-34)
+    const float t = acc + shfl_xor(acc, 4);
+    const float u = t + shfl_xor(t, 2);
+    const float v = u + shfl_xor(u, 1);
+    const int grow = grow0 + rr;
+    if (rr < R && chain == 0 && grow < a.total_rows) store_row(a, grow, tok, v);
+}
+
 // ------------------------------------------------------- F16 / BF16 / F32
 template <int KIND>
 __device__ __forceinline__ float wval(const uint8_t *row, size_t i) {
@@ -885,16 +1022,31 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
         launch_kq<AOTK_Q6_K>(a, grid, s);
         break;
     case AOTK_Q8_0:
-        grid.x = (unsigned)((a.total_rows + 31) / 32);
-        k_mv_q80<AOTK_Q8_0><<<grid, 256, 0, s>>>(a);
+        if (a.cols <= (size_t)Q8B_MAX_COLS) {
+            grid.x = (unsigned)((a.total_rows + 4 * Q8B_R - 1) / (4 * Q8B_R));
+            k_mv_q8b<AOTK_Q8_0><<<grid, 256, 0, s>>>(a);
+        } else {
+            grid.x = (unsigned)((a.total_rows + 31) / 32);
+            k_mv_q80<AOTK_Q8_0><<<grid, 256, 0, s>>>(a);
+        }
         break;
     case AOTK_Q4_0:
-        grid.x = (unsigned)((a.total_rows + 31) / 32);
-        k_mv_q80<AOTK_Q4_0><<<grid, 256, 0, s>>>(a);
+        if (a.cols <= (size_t)Q8B_MAX_COLS) {
+            grid.x = (unsigned)((a.total_rows + 4 * Q8B_R - 1) / (4 * Q8B_R));
+            k_mv_q8b<AOTK_Q4_0><<<grid, 256, 0, s>>>(a);
+        } else {
+            grid.x = (unsigned)((a.total_rows + 31) / 32);
+            k_mv_q80<AOTK_Q4_0><<<grid, 256, 0, s>>>(a);
+        }
         break;
     case AOTK_Q5_0:
-        grid.x = (unsigned)((a.total_rows + 31) / 32);
-        k_mv_q80<AOTK_Q5_0><<<grid, 256, 0, s>>>(a);
+        if (a.cols <= (size_t)Q8B_MAX_COLS) {
+            grid.x = (unsigned)((a.total_rows + 4 * Q8B_R - 1) / (4 * Q8B_R));
+            k_mv_q8b<AOTK_Q5_0><<<grid, 256, 0, s>>>(a);
+        } else {
+            grid.x = (unsigned)((a.total_rows + 31) / 32);
+            k_mv_q80<AOTK_Q5_0><<<grid, 256, 0, s>>>(a);
+        }
         break;
     case AOTK_F16:
         grid.x = (unsigned)((a.total_rows + 31) / 32);
