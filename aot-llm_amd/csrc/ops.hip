@@ -452,23 +452,30 @@ __global__ __launch_bounds__(576) void k_attn_qk_decode(AttnArgs a, QkvPost p) {
 //   thread for short spans, the exact parallel replay for spans of
 //   SV_SEQ_MIN..SEQ_MAX_N), multiply by 1/sum; the blocks of one head repeat
 //   it identically;
-//   output (ops.rs:209-215): chunks of SV_CP positions: all threads form the
-//   products p_t * v_t,d into LDS (float4 V loads issued SV_PD chunks ahead),
-//   then thread d adds them in position order while the others form the
-//   next chunk.
+//   output (ops.rs:209-215): chunks of CP positions: all threads form the
+//   products p_t * v_t,d into LDS, dim-major (row of dim d: CP products and
+//   4 pad floats), with the float4 V loads issued PD chunks ahead; then
+//   thread d adds its row in position order (float4 LDS reads one group of
+//   16 ahead of the adds) while the others form the next chunk.
 #ifndef ATT_TS
 #define ATT_TS(i)
 #endif
+#ifndef SV_TS
+#define SV_TS(c, i)
+#endif
 constexpr int ATT_MAX_SPAN = 16384;
-constexpr int SV_BUF = 8192;      // floats per product buffer
 constexpr int SV_DB = 32;         // dims per block
+constexpr int SV_CP = 240;        // positions per chunk
+constexpr int SV_RS = SV_CP + 4;  // floats per dim row of the product buffer
+constexpr int SV_BUF = SV_DB * SV_RS;  // floats per product buffer
 constexpr int SV_SEQ_MIN = 2048;  // shorter spans are summed by one thread
 template <int HD>
 __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     constexpr int DB = SV_DB;
-    constexpr int CP = SV_BUF / DB;
+    constexpr int CP = SV_CP;
     __shared__ __align__(16) float e[ATT_MAX_SPAN + 64];
-    __shared__ __align__(16) uint8_t ubuf[sizeof(SeqScratch) > 2 * SV_BUF * 4 ? sizeof(SeqScratch) : 2 * SV_BUF * 4];
+    // product buffers (+32 floats read past the end by the last group) / sum scratch
+    __shared__ __align__(16) uint8_t ubuf[sizeof(SeqScratch) > (2 * SV_BUF + 32) * 4 ? sizeof(SeqScratch) : (2 * SV_BUF + 32) * 4];
     __shared__ float red[SEQ_T / 64];
     __shared__ float bc;
     SeqScratch &S = *reinterpret_cast<SeqScratch *>(ubuf);
@@ -515,22 +522,25 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     const size_t kv = (size_t)a.n_kv_head * HD;
     const float *vb = a.v_cache + t0 * kv + (size_t)kvh * HD + d0;
     constexpr int R4 = DB / 4;
-    static_assert(CP * R4 == 2 * SEQ_T, "two float4 per thread per chunk");
-    // V loads run SV_PD chunks ahead of the products (a register ring)
+    constexpr int NPROD = SEQ_T - 64;  // waves 1.. form the products, wave 0 adds them
+    static_assert(CP * R4 == 2 * NPROD, "two float4 per producer thread per chunk");
+    // V loads run PD chunks ahead of the products (a register ring)
     constexpr int PD = 8;
     float4 ring[PD][2];
+    const int pid = tid - 64;
     auto issue = [&](float4 (&dst)[2], int c) {
 #pragma unroll
         for (int k = 0; k < 2; k++) {
-            const int idx = tid + k * SEQ_T;
+            const int idx = pid + k * NPROD;
             const int t = c * CP + idx / R4;
             dst[k] = t < cnt ? *(const float4 *)(vb + (size_t)t * kv + 4 * (idx % R4)) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
     };
     float o = 0.0f;
     const int nch = (cnt + CP - 1) / CP;
+    if (pid >= 0)
 #pragma unroll
-    for (int j = 0; j < PD; j++) issue(ring[j], j);
+        for (int j = 0; j < PD; j++) issue(ring[j], j);
     for (int c0 = 0; c0 < nch; c0 += PD) {
 #pragma unroll
         for (int j = 0; j < PD; j++) {
@@ -539,28 +549,56 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
                 float *buf = prod + (c & 1) * SV_BUF;
                 const int base = c * CP;
                 const int rows = min(CP, cnt - base);
+                if (pid >= 0) {
 #pragma unroll
-                for (int k = 0; k < 2; k++) {
-                    const int idx = tid + k * SEQ_T;
-                    const int r = idx / R4;
-                    const float pt = r < rows ? e[at(base + r)] : 0.0f;
-                    const float4 v4 = ring[j][k];
-                    *(float4 *)(buf + idx * 4) = make_float4(pt * v4.x, pt * v4.y, pt * v4.z, pt * v4.w);
-                }
-                issue(ring[j], c + PD);
-                __syncthreads();
-                if (tid < DB) {
-                    const float *bp = buf + tid;
-                    int r = 0;
-                    for (; r + 16 <= rows; r += 16) {
-                        float v[16];
-#pragma unroll
-                        for (int k = 0; k < 16; k++) v[k] = bp[(r + k) * DB];
-#pragma unroll
-                        for (int k = 0; k < 16; k++) o += v[k];
+                    for (int k = 0; k < 2; k++) {
+                        const int idx = pid + k * NPROD;
+                        const int r = idx / R4, d = 4 * (idx % R4);
+                        const float pt = r < rows ? e[at(base + r)] : 0.0f;
+                        const float4 v4 = ring[j][k];
+                        buf[(d + 0) * SV_RS + r] = pt * v4.x;
+                        buf[(d + 1) * SV_RS + r] = pt * v4.y;
+                        buf[(d + 2) * SV_RS + r] = pt * v4.z;
+                        buf[(d + 3) * SV_RS + r] = pt * v4.w;
                     }
-                    for (; r < rows; r++) o += bp[r * DB];
+                    issue(ring[j], c + PD);
                 }
+                SV_TS(c, 0);
+                __syncthreads();
+                SV_TS(c, 1);
+                if (tid < DB) {
+                    // groups of 16 in two register sets, each set loaded one
+                    // group ahead of its adds
+                    const float4 *bp = (const float4 *)(buf + tid * SV_RS);
+                    int full = rows & ~31;
+                    float4 ga[4], gb[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) ga[k] = bp[k];
+                    for (int r = 0; r < full; r += 32) {
+#pragma unroll
+                        for (int k = 0; k < 4; k++) gb[k] = bp[r / 4 + 4 + k];
+#pragma unroll
+                        for (int k = 0; k < 4; k++) {
+                            o += ga[k].x; o += ga[k].y; o += ga[k].z; o += ga[k].w;
+                        }
+#pragma unroll
+                        for (int k = 0; k < 4; k++) ga[k] = bp[r / 4 + 8 + k];  // past the end on the last group: unused
+#pragma unroll
+                        for (int k = 0; k < 4; k++) {
+                            o += gb[k].x; o += gb[k].y; o += gb[k].z; o += gb[k].w;
+                        }
+                    }
+                    if (rows - full >= 16) {  // ga holds the group at `full`
+#pragma unroll
+                        for (int k = 0; k < 4; k++) {
+                            o += ga[k].x; o += ga[k].y; o += ga[k].z; o += ga[k].w;
+                        }
+                        full += 16;
+                    }
+                    const float *tp = buf + tid * SV_RS;
+                    for (int r = full; r < rows; r++) o += tp[r];
+                }
+                SV_TS(c, 2);
             }
         }
     }
