@@ -606,6 +606,136 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     if (tid < DB) a.out[i * (size_t)a.n_head * HD + (size_t)h * HD + d0 + tid] = o;
 }
 
+// Batched rows (prompt chunks), spans up to ATT_ROWS_MAX: the same softmax
+// and output, with the serial chains spread over lanes instead of blocks.
+//   k_attn_softmax_rows: one wave per (row, head): max, glibc-matched exp
+//   into LDS, the sequential sum by lane 0, then p = e * (1 / sum) written
+//   back over the scores.
+//   k_attn_out_rows: one wave per (head, 64-dim slice, ATT_RB rows); lane d
+//   keeps the ATT_RB sums of dim d and adds p_t * v_t,d in position order;
+//   V rows are read straight from the cache (256 B per wave per position),
+//   the probabilities with wave-uniform loads.
+constexpr int ATT_ROWS_MAX = 2048;
+constexpr int ATT_RB = 4;
+
+__global__ __launch_bounds__(256) void k_attn_softmax_rows(AttnArgs a, int m) {
+    __shared__ __align__(16) float e[4][ATT_ROWS_MAX];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int pair = blockIdx.x * 4 + w;
+    if (pair >= m * a.n_head) return;
+    const int i = pair / a.n_head, h = pair % a.n_head;
+    size_t t0, n;
+    row_range(a, i, t0, n);
+    const int cnt = (int)(n - t0);
+    float *ps = a.prob + ((size_t)i * a.n_head + h) * a.span;
+    float *ew = e[w];
+    float mx = -INFINITY;
+    for (int t = lane; t < cnt; t += 64) {
+        const float v = ps[t];
+        ew[t] = v;
+        mx = fmaxf(mx, v);
+    }
+    mx = wave_max(mx);
+    for (int t = lane; t < cnt; t += 64) ew[t] = aotk_expf(ew[t] - mx);
+    wave_lds_sync();
+    float sum = 0.0f;
+    if (lane == 0) sum = seq_sum_lds<false>(ew, cnt);
+    const float inv = 1.0f / readlane_f(sum, 0);
+    for (int t = lane; t < cnt; t += 64) ps[t] = ew[t] * inv;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_out_rows(AttnArgs a, int m) {
+    constexpr int NS = HD / 64;
+    const int lane = threadIdx.x & 63;
+    const int task = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int slice = task % NS, h = (task / NS) % a.n_head, rg = task / (NS * a.n_head);
+    if (rg * ATT_RB >= m) return;
+    const int gqa = a.n_head / a.n_kv_head, kvh = h / gqa;
+    const size_t kv = (size_t)a.n_kv_head * HD;
+    const int d = slice * 64 + lane;
+    int row[ATT_RB];
+    size_t t0[ATT_RB], tn[ATT_RB];
+    const float *pr[ATT_RB];
+    size_t lo = ~(size_t)0, hi = 0, alo = 0, ahi = ~(size_t)0;
+#pragma unroll
+    for (int r = 0; r < ATT_RB; r++) {
+        row[r] = min(rg * ATT_RB + r, m - 1);  // rows past m repeat the last one, unstored
+        row_range(a, row[r], t0[r], tn[r]);
+        pr[r] = a.prob + ((size_t)row[r] * a.n_head + h) * a.span - t0[r];
+        lo = min(lo, t0[r]);
+        hi = max(hi, tn[r]);
+        alo = max(alo, t0[r]);
+        ahi = min(ahi, tn[r]);
+    }
+    const float *vb = a.v_cache + (size_t)kvh * HD + d;
+    float o[ATT_RB];
+#pragma unroll
+    for (int r = 0; r < ATT_RB; r++) o[r] = 0.0f;
+    auto step_if = [&](size_t t) {
+        const float v = vb[t * kv];
+#pragma unroll
+        for (int r = 0; r < ATT_RB; r++)
+            if (t >= t0[r] && t < tn[r]) o[r] += pr[r][t] * v;
+    };
+    if (alo >= ahi) {  // no position common to all rows
+        for (size_t t = lo; t < hi; t++) step_if(t);
+    } else {
+        for (size_t t = lo; t < alo; t++) step_if(t);
+        // groups of 32 positions in two register sets (A, B), each loaded one
+        // group ahead of its use: V with one load per position, p with one
+        // load per row (lane k holds position k) broadcast by readlane
+        size_t t = alo;
+        float va[32], pa[ATT_RB], vbb[32], pb[ATT_RB];
+        auto load = [&](float (&v)[32], float (&pv)[ATT_RB], size_t c) {
+#pragma unroll
+            for (int k = 0; k < 32; k++) v[k] = vb[(c + k) * kv];
+#pragma unroll
+            for (int r = 0; r < ATT_RB; r++) pv[r] = pr[r][c + (lane & 31)];
+        };
+        auto use = [&](const float (&v)[32], const float (&pv)[ATT_RB]) {
+#pragma unroll
+            for (int k = 0; k < 32; k++)
+#pragma unroll
+                for (int r = 0; r < ATT_RB; r++) o[r] += readlane_f(pv[r], k) * v[k];
+        };
+        if (t + 32 <= ahi) load(va, pa, t);
+        while (t + 32 <= ahi) {
+            const bool more = t + 64 <= ahi;
+            if (more) load(vbb, pb, t + 32);
+            use(va, pa);
+            t += 32;
+            if (!more) break;
+            const bool more2 = t + 64 <= ahi;
+            if (more2) load(va, pa, t + 32);
+            use(vbb, pb);
+            t += 32;
+            if (!more2) break;
+        }
+        for (; t < ahi; t++) {
+            const float v = vb[t * kv];
+#pragma unroll
+            for (int r = 0; r < ATT_RB; r++) o[r] += pr[r][t] * v;
+        }
+        for (t = ahi; t < hi; t++) step_if(t);
+    }
+#pragma unroll
+    for (int r = 0; r < ATT_RB; r++)
+        if (rg * ATT_RB + r < m) a.out[(size_t)row[r] * a.n_head * HD + (size_t)h * HD + d] = o[r];
+}
+
+static void launch_rows(const AttnArgs &a, size_t head_dim, size_t m, hipStream_t s) {
+    const unsigned pairs = (unsigned)(m * a.n_head);
+    k_attn_softmax_rows<<<(pairs + 3) / 4, 256, 0, s>>>(a, (int)m);
+    const size_t tasks = (m + ATT_RB - 1) / ATT_RB * a.n_head * (head_dim / 64);
+    const unsigned g = (unsigned)((tasks + 3) / 4);
+    switch (head_dim) {
+    case 64: k_attn_out_rows<64><<<g, 256, 0, s>>>(a, (int)m); break;
+    case 128: k_attn_out_rows<128><<<g, 256, 0, s>>>(a, (int)m); break;
+    default: k_attn_out_rows<256><<<g, 256, 0, s>>>(a, (int)m); break;
+    }
+}
+
 static void launch_sv(const AttnArgs &a, size_t head_dim, size_t m, hipStream_t s) {
     dim3 g((unsigned)(a.n_head * (head_dim / SV_DB)), (unsigned)m);
     switch (head_dim) {
@@ -654,7 +784,13 @@ void launch_attention(float *out, const float *q, const float *k_cache, const fl
     case 128: k_attn_scores<128><<<grid, threads, 0, s>>>(a); break;
     default: k_attn_scores<256><<<grid, threads, 0, s>>>(a); break;
     }
-    launch_sv(a, head_dim, m, s);
+    // the longest row spans min(pos0 + m, window) positions
+    const size_t longest = window > 0 && window < pos0 + m ? window : pos0 + m;
+    static const bool rows_off = getenv("AOTK_NO_ATT_ROWS") != nullptr;  // the per-block path, for comparison
+    if (m > 1 && !pos_dev && longest <= (size_t)ATT_ROWS_MAX && !rows_off)
+        launch_rows(a, head_dim, m, s);
+    else
+        launch_sv(a, head_dim, m, s);
 }
 
 void launch_attention_decode(float *out, const QkvPost &p, size_t ctx_rows, size_t pos0, size_t window,
