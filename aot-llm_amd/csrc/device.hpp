@@ -9,28 +9,14 @@
 
 namespace aotk {
 
-// IEEE binary16 -> f32 (crates/aot-kernels/src/quant.rs:96-125), integer
-// form so NaN payloads and subnormals match the reference bit for bit.
+// IEEE binary16 -> f32 (crates/aot-kernels/src/quant.rs:96-125). Zeros,
+// subnormals and normals convert exactly in hardware (v_cvt_f32_f16, f16
+// denormals on); infinities and NaNs take the integer form so that NaN
+// payloads match the reference bit for bit (the hardware quiets them).
 __device__ __forceinline__ float f16_to_f32(uint32_t h) {
-    uint32_t sign = (h & 0x8000u) << 16;
-    uint32_t exp = (h >> 10) & 0x1Fu;
-    uint32_t mant = h & 0x3FFu;
-    uint32_t bits;
-    if (exp == 0) {
-        if (mant == 0) {
-            bits = sign;
-        } else {
-            // value = mant * 2^-24; normalise: leading bit k -> exponent k + 103.
-            uint32_t lz = __builtin_clz(mant) - 21;  // shifts to bring bit 10 up
-            uint32_t m = mant << lz;
-            bits = sign | ((113u - lz) << 23) | ((m & 0x3FFu) << 13);
-        }
-    } else if (exp == 31) {
-        bits = sign | 0x7F800000u | (mant << 13);
-    } else {
-        bits = sign | ((exp + 112u) << 23) | (mant << 13);
-    }
-    return __uint_as_float(bits);
+    const float hw = (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
+    const uint32_t special = ((h & 0x8000u) << 16) | 0x7F800000u | ((h & 0x3FFu) << 13);
+    return (h & 0x7C00u) == 0x7C00u ? __uint_as_float(special) : hw;
 }
 
 // f32 -> binary16, round to nearest even (quant.rs:128-162).

@@ -352,13 +352,17 @@ __device__ __forceinline__ float kq_term(const uint4 (&c)[KqGeom<KIND>::CH], flo
 
 // PF = 0: one row group per wave (G == 1), register budget for 4 waves per
 // SIMD; PF = 1: G groups per wave with the next group's loads in flight.
-template <int KIND, int PF>
+// NB > 0: the super-blocks per row as a compile-time constant (immediate
+// chunk offsets, constant row-slot division, an unmasked fold); NB == 0 reads
+// it from the arguments.
+template <int KIND, int PF, int NB>
 __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int bx, uint8_t *sY, float (*sT)[256 + 16]) {
     using Geo = KqGeom<KIND>;
     constexpr int CH = Geo::CH;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tok = blockIdx.y;
-    const int nb = a.nb;
+    const int nb = NB > 0 ? NB : a.nb;
+    if (NB > 0) RL = 64 / NB;
     const int rs = lane / nb, s = lane - rs * nb;
     const bool lane_on = rs < RL;
     const int sa = lane_on ? s : 0;
@@ -382,6 +386,12 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
         if (KIND == AOTK_Q6_K)
             d6 = f16_to_f32(((const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]))[(size_t)local * nb + sa]);
     };
+#ifdef MV_STAGGER
+    {
+        const int batch = (int)((bx * 4 + wave) / MV_STAGGER);
+        for (int i = 0; i < batch; i++) __builtin_amdgcn_s_sleep(10);
+    }
+#endif
     MV_TS(0);
     load(cur, dcur, 0);  // weights first: the longest latency
     // stage this token's Q8_K activation in LDS
@@ -400,7 +410,14 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
     // at a time ahead of the dependent adds), the store
     auto group = [&](const uint4 *c, float d6, int gi) {
         const int gr0 = (group0 + gi) * RL;
+#ifdef MV_LOADONLY
+        uint32_t xx = 0;
+#pragma unroll
+        for (int k = 0; k < CH; k++) xx ^= c[k].x ^ c[k].y ^ c[k].z ^ c[k].w;
+        const float term = (float)(xx & 1u) + d6 + (float)rec[0];
+#else
         const float term = kq_term<KIND>(*(const uint4(*)[CH])c, d6, rec);
+#endif
         MV_TS(2 + 2 * gi);
         if (lane_on) sT[wave][rs * ts + s] = term;
         wave_lds_sync();
@@ -444,21 +461,34 @@ struct KqShared {
     __align__(16) float t[4][256 + 16];  // [wave][row slot * ts + super-block] (+ read slack)
 };
 
-template <int KIND, int PF>
+template <int KIND, int PF, int NB>
 __global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq(MvArgs a, int RL, int G) {
     __shared__ KqShared sh;
-    mv_kq_body<KIND, PF>(a, RL, G, blockIdx.x, sh.y, sh.t);
+    mv_kq_body<KIND, PF, NB>(a, RL, G, blockIdx.x, sh.y, sh.t);
 }
 
 // Two K-quant matrices of different kinds sharing the input in one launch
 // (q/k in one kind and v in another): blocks [0, nblk_a) run `a`, the rest
 // run `b`.
-template <int KA, int KB>
+template <int KA, int KB, int NB>
 __global__ __launch_bounds__(256, 2) void k_mv_kq2(MvArgs a, int RLa, int Ga, MvArgs b, int RLb, int Gb, int nblk_a) {
     __shared__ KqShared sh;
-    if ((int)blockIdx.x < nblk_a) mv_kq_body<KA, 1>(a, RLa, Ga, blockIdx.x, sh.y, sh.t);
-    else mv_kq_body<KB, 1>(b, RLb, Gb, blockIdx.x - nblk_a, sh.y, sh.t);
+    if ((int)blockIdx.x < nblk_a) mv_kq_body<KA, 1, NB>(a, RLa, Ga, blockIdx.x, sh.y, sh.t);
+    else mv_kq_body<KB, 1, NB>(b, RLb, Gb, blockIdx.x - nblk_a, sh.y, sh.t);
 }
+
+// The row lengths of the configs (cols / 256) get their own instantiations.
+#define AOTK_NB_SWITCH(nb, F) \
+    switch (nb) {             \
+    case 8: F(8); break;      \
+    case 10: F(10); break;    \
+    case 16: F(16); break;    \
+    case 22: F(22); break;    \
+    case 40: F(40); break;    \
+    case 48: F(48); break;    \
+    case 56: F(56); break;    \
+    default: F(0); break;     \
+    }
 
 // ------------------------------------------------- K-quant matmul (MFMA)
 // Prompt batches (m tokens, 2 <= m <= 64): block = 16 weight rows x 64
@@ -518,49 +548,54 @@ __device__ __forceinline__ void mm_load(MmW<KIND> &w, const uint8_t *rowp, const
     }
 }
 
-template <int KIND>
+template <int KIND, int TT>
 __global__ __launch_bounds__(256) void k_mm_kq(MvArgs a, int m) {
-    __shared__ __align__(16) uint8_t sY[3][MM_TOK * MM_YS];
-    __shared__ float sD[3][MM_TOK];
+    constexpr int NT = 16 * TT;  // tokens per block
+    __shared__ __align__(16) uint8_t sY[3][NT * MM_YS];
+    __shared__ float sD[3][NT];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int q = lane >> 4, r16 = lane & 15;
     const int nb = a.nb;
-    const int grow = blockIdx.x * 16 + r16;  // this lane's weight row
+    const int grow = blockIdx.x * 64 + wave * 16 + r16;  // this lane's weight row
+    const int tok0 = blockIdx.y * NT;                    // the block's first token
+    const int mt = min(NT, m - tok0);                    // tokens of this block
     const bool row_ok = grow < a.total_rows;
     int local;
     const int sg = seg_of(a, row_ok ? grow : 0, local);
     const size_t rowb = (size_t)nb * KqGeom<KIND>::RB;
     const uint8_t *rowp = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * rowb;
     const uint16_t *drow = KIND == AOTK_Q6_K ? (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb : nullptr;
-    const int t = wave;                       // this wave's token tile
-    const bool tile_on = 16 * t < m;
 
-    // activation staging: tokens x 256 bytes + d of super-block sb, two
+    // activation staging: NT tokens x 256 bytes + d of super-block sb, two
     // super-blocks ahead (register sets r0 / r1, LDS ring of 3)
     struct Stg {
-        uint4 v[4];
+        uint4 v[TT];
         float d;
     };
     auto stage_load = [&](Stg &r, int sb) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int idx = tid + 256 * k;  // 64 tokens x 16 uint4
+        for (int k = 0; k < TT; k++) {
+            const int idx = tid + 256 * k;  // NT tokens x 16 uint4
             const int tk = idx >> 4, c = idx & 15;
-            r.v[k] = tk < m ? *(const uint4 *)(a.xq + (size_t)tk * a.cols + (size_t)sb * 256 + 16 * c) : make_uint4(0, 0, 0, 0);
+            r.v[k] = tk < mt ? *(const uint4 *)(a.xq + (size_t)(tok0 + tk) * a.cols + (size_t)sb * 256 + 16 * c) : make_uint4(0, 0, 0, 0);
         }
-        r.d = (tid < MM_TOK && tid < m) ? a.xd[(size_t)tid * nb + sb] : 0.0f;
+        r.d = (tid < mt) ? a.xd[(size_t)(tok0 + tid) * nb + sb] : 0.0f;
     };
     auto stage_store = [&](const Stg &r, int buf) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < TT; k++) {
             const int idx = tid + 256 * k;
             const int tk = idx >> 4, c = idx & 15;
             *(uint4 *)(sY[buf] + tk * MM_YS + 16 * c) = r.v[k];
         }
-        if (tid < MM_TOK) sD[buf][tid] = r.d;
+        if (tid < NT) sD[buf][tid] = r.d;
     };
 
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[TT][4];
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[t][i] = 0.0f;
 
     MmW<KIND> cur, nxt, nx2;
     Stg r0, r1;
@@ -588,7 +623,8 @@ __global__ __launch_bounds__(256) void k_mm_kq(MvArgs a, int m) {
 #pragma unroll
             for (int j = 0; j < 8; j++) scale_min_k4(j, cur.hdr.y, cur.hdr.z, cur.hdr.w, sc[j], mn[j]);
         }
-        // B fragments (the lane's 8 values of each 32-value step j)
+        // B fragments (the lane's 8 values of each 32-value step j), shared
+        // by the block's token tiles
         long bq[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -618,8 +654,21 @@ __global__ __launch_bounds__(256) void k_mm_kq(MvArgs a, int m) {
             }
             bq[j] = (long)(((unsigned long)w1 << 32) | w0);
         }
+        long mb[8];
+        if (KIND != AOTK_Q6_K)
+#pragma unroll
+            for (int j = 0; j < 8; j++) mb[j] = (long)(0x0101010101010101ULL * (unsigned long)mn[j]);
+        float dd = 0.0f, dm = 0.0f;
+        if (KIND == AOTK_Q6_K) {
+            dd = cur.d6;
+        } else {
+            dd = f16_to_f32(cur.hdr.x & 0xFFFFu);
+            dm = f16_to_f32(cur.hdr.x >> 16);
+        }
         const uint8_t *ys = sY[buf];
-        if (tile_on) {
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            if (16 * t >= mt) break;
             // A fragments: token 16t + r16, k = 32j + 8q .. +8
             const uint8_t *yrow = ys + (16 * t + r16) * MM_YS + 8 * q;
             int sumi[4] = {0, 0, 0, 0};
@@ -640,8 +689,7 @@ __global__ __launch_bounds__(256) void k_mm_kq(MvArgs a, int m) {
                     c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bq[j], c, 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; i++) sumi[i] += __mul24(sc[j], c[i]);
-                    const long mb = (long)(0x0101010101010101ULL * (unsigned long)mn[j]);
-                    csum = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, mb, csum, 0, 0, 0);
+                    csum = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, mb[j], csum, 0, 0, 0);
                 }
             }
             // fold: tokens 16t + 4q + i of the lane's row
@@ -650,14 +698,11 @@ __global__ __launch_bounds__(256) void k_mm_kq(MvArgs a, int m) {
                 const float yd = sD[buf][16 * t + 4 * q + i];
                 float term;
                 if (KIND == AOTK_Q6_K) {
-                    const float dd = cur.d6 * yd;
-                    term = dd * (float)sumi[i];
+                    term = (dd * yd) * (float)sumi[i];
                 } else {
-                    const float dd = f16_to_f32(cur.hdr.x & 0xFFFFu) * yd;
-                    const float dm = f16_to_f32(cur.hdr.x >> 16) * yd;
-                    term = dd * (float)sumi[i] - dm * (float)csum[i];
+                    term = (dd * yd) * (float)sumi[i] - (dm * yd) * (float)csum[i];
                 }
-                acc[i] = acc[i] + term;
+                acc[t][i] = acc[t][i] + term;
             }
         }
         if (sb + 1 < nb) stage_store(r1, (sb + 1) % 3);
@@ -666,12 +711,14 @@ __global__ __launch_bounds__(256) void k_mm_kq(MvArgs a, int m) {
         nxt = nx2;
         r1 = r0;
     }
-    if (row_ok && tile_on) {
+    if (row_ok) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int tok = 16 * t + 4 * q + i;
-            if (tok < m) store_row(a, grow, tok, acc[i]);
-        }
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tk = 16 * t + 4 * q + i;
+                if (tk < mt) store_row(a, grow, tok0 + tk, acc[t][i]);
+            }
     }
 }
 
@@ -977,8 +1024,7 @@ static MvArgs make_args(int n, const DevWeight *const ws[], float *const ys[], c
 // K-quant kernel: all waves resident in one round (3 waves per SIMD on 256
 // CUs), each doing G row groups.
 static void kq_shape(const MvArgs &a, int &RL, int &G, int &blocks) {
-    RL = 1;
-    while (RL * 2 * a.nb <= 64) RL *= 2;
+    RL = 64 / a.nb;  // rows per group: every lane slot of nb lanes that fits
     const int groups = (a.total_rows + RL - 1) / RL;
     G = (groups + 3071) / 3072;
     G = G > 8 ? 8 : G;
@@ -991,7 +1037,9 @@ static void launch_kq(const MvArgs &a, dim3 grid, hipStream_t s) {
         int RL, G, blocks;
         kq_shape(a, RL, G, blocks);
         grid.x = (unsigned)blocks;
-        k_mv_kq<KIND, 1><<<grid, 256, 0, s>>>(a, RL, G);
+#define F(NB) k_mv_kq<KIND, 1, NB><<<grid, 256, 0, s>>>(a, RL, G)
+        AOTK_NB_SWITCH(a.nb, F)
+#undef F
     } else {
         grid.x = (unsigned)((a.total_rows + 7) / 8);
         k_mv_kquant<KIND, 2><<<grid, 256, 0, s>>>(a);
@@ -1003,12 +1051,26 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
     grid.y = (unsigned)m;
     if (m >= MM_MIN_TOKENS && m <= MM_TOK && (kind == AOTK_Q4_K || kind == AOTK_Q5_K || kind == AOTK_Q6_K) &&
         !getenv("AOTK_NO_MFMA")) {
-        dim3 g((unsigned)((a.total_rows + 15) / 16), 1);
+        // 64 rows per block; the token tiles per block are cut until the
+        // grid reaches 512 blocks (small matrices) or one tile is left
+        const unsigned rb = (unsigned)((a.total_rows + 63) / 64);
+        const int tiles = (int)((m + 15) / 16);
+        int tt = tiles;
+        while (tt > 1 && rb * (unsigned)((tiles + tt - 1) / tt) < 512) tt = (tt + 1) / 2;
+        dim3 g(rb, (unsigned)((tiles + tt - 1) / tt));
+#define MMK(K)                                                      \
+    switch (tt) {                                                   \
+    case 1: k_mm_kq<K, 1><<<g, 256, 0, s>>>(a, (int)m); break;      \
+    case 2: k_mm_kq<K, 2><<<g, 256, 0, s>>>(a, (int)m); break;      \
+    case 3: k_mm_kq<K, 3><<<g, 256, 0, s>>>(a, (int)m); break;      \
+    default: k_mm_kq<K, 4><<<g, 256, 0, s>>>(a, (int)m); break;     \
+    }
         switch (kind) {
-        case AOTK_Q4_K: k_mm_kq<AOTK_Q4_K><<<g, 256, 0, s>>>(a, (int)m); break;
-        case AOTK_Q5_K: k_mm_kq<AOTK_Q5_K><<<g, 256, 0, s>>>(a, (int)m); break;
-        default: k_mm_kq<AOTK_Q6_K><<<g, 256, 0, s>>>(a, (int)m); break;
+        case AOTK_Q4_K: MMK(AOTK_Q4_K) break;
+        case AOTK_Q5_K: MMK(AOTK_Q5_K) break;
+        default: MMK(AOTK_Q6_K) break;
         }
+#undef MMK
         return;
     }
     switch (kind) {
@@ -1096,10 +1158,15 @@ void launch_matvec_pair(int na, const DevWeight *const wa[], float *const ya[], 
     kq_shape(a, RLa, Ga, na_blk);
     kq_shape(b, RLb, Gb, nb_blk);
     dim3 grid((unsigned)(na_blk + nb_blk), (unsigned)m);
-    if (wa[0]->kind == AOTK_Q4_K)
-        k_mv_kq2<AOTK_Q4_K, AOTK_Q6_K><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk);
-    else
-        k_mv_kq2<AOTK_Q5_K, AOTK_Q6_K><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk);
+    if (wa[0]->kind == AOTK_Q4_K) {
+#define F(NB) k_mv_kq2<AOTK_Q4_K, AOTK_Q6_K, NB><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk)
+        AOTK_NB_SWITCH(a.nb, F)
+#undef F
+    } else {
+#define F(NB) k_mv_kq2<AOTK_Q5_K, AOTK_Q6_K, NB><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk)
+        AOTK_NB_SWITCH(a.nb, F)
+#undef F
+    }
 }
 
 }  // namespace aotk

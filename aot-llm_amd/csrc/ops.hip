@@ -102,6 +102,9 @@ __device__ __forceinline__ ActQ8_0 q80_row(ActQ8_0 a, size_t row, size_t n) {
 
 // rmsnorm (ops.rs:7-18) of row blockIdx.x, then quantization of the result.
 // n % 256 == 0, n <= 8192 (the normalised row is staged in LDS).
+#ifndef RMS_TS
+#define RMS_TS(i)
+#endif
 __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant(const float *__restrict__ x, const float *__restrict__ w, int n,
                                                          float eps, RmsOut out) {
     __shared__ __align__(16) float row[8192];
@@ -110,6 +113,7 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant(const float *__restrict
     const size_t m = blockIdx.x;
     const float *xr = x + m * n;
     const int C = seq_chunk(n);
+    RMS_TS(0);
     // the norm weights are loaded before the sum (n <= 8 * blockDim.x)
     float wv[8];
 #pragma unroll
@@ -123,7 +127,9 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant(const float *__restrict
         sq[seq_idx(i, C)] = v * v;
     }
     __syncthreads();
+    RMS_TS(1);
     float ss = exact_seq_sum(sq, n, S);
+    RMS_TS(2);
     float r = 1.0f / sqrtf(ss / (float)n + eps);
 #pragma unroll
     for (int k = 0; k < 8; k++) {
@@ -143,6 +149,7 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant(const float *__restrict
         float v[4] = {v4.x, v4.y, v4.z, v4.w};
         quant256(v, lane, b, qk, q0);
     }
+    RMS_TS(3);
 }
 
 void launch_rmsnorm_quant(const float *x, const float *w, size_t n, size_t m, float eps, RmsOut out, hipStream_t s) {
@@ -833,7 +840,9 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_add(float *x, const float *y,
         sq[seq_idx(i, C)] = v * v;
     }
     __syncthreads();
+    RMS_TS(1);
     float ss = exact_seq_sum(sq, n, S);
+    RMS_TS(2);
     float r = 1.0f / sqrtf(ss / (float)n + eps);
     for (int i = threadIdx.x; i < n; i += blockDim.x) xr[i] = xr[i] + row[i] * r * w[i];
 }

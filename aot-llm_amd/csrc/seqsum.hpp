@@ -41,7 +41,8 @@ constexpr int SEQ_MAX_N = 8192;
 // lanes of a wave walking their chunks spread over the banks.
 constexpr int SEQ_T = 1024;
 constexpr int SEQ_PAD_N = SEQ_MAX_N + SEQ_T + 32;
-__device__ __forceinline__ int seq_threads(int n) { return n <= 1024 ? 256 : SEQ_T; }
+constexpr int SEQ_MID_N = 4096;  // sums up to this length run on 512 threads
+__device__ __forceinline__ int seq_threads(int n) { return n <= 1024 ? 256 : (n <= SEQ_MID_N ? 512 : SEQ_T); }
 __device__ __forceinline__ int seq_chunk(int n) { return (n + seq_threads(n) - 1) / seq_threads(n); }
 __device__ __forceinline__ int seq_idx(int k, int C) { return (k / C) * (C + 1) + (k % C); }
 constexpr int SEQ_MAX_EV = 2048;
@@ -343,6 +344,7 @@ __device__ __forceinline__ float exact_seq_sum_t(const float *pp, int n, SeqScra
 __device__ __forceinline__ float exact_seq_sum(const float *pp, int n, SeqScratch &S) {
     const int C = seq_chunk(n);
     if (seq_threads(n) == 256) return exact_seq_sum_t<4, 256>(pp, n, S);
+    if (seq_threads(n) == 512) return exact_seq_sum_t<8, 512>(pp, n, S);
     if (C <= 4) return exact_seq_sum_t<4, SEQ_T>(pp, n, S);
     return exact_seq_sum_t<SEQ_MAX_N / SEQ_T, SEQ_T>(pp, n, S);
 }
