@@ -386,12 +386,6 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
         if (KIND == AOTK_Q6_K)
             d6 = f16_to_f32(((const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]))[(size_t)local * nb + sa]);
     };
-#ifdef MV_STAGGER
-    {
-        const int batch = (int)((bx * 4 + wave) / MV_STAGGER);
-        for (int i = 0; i < batch; i++) __builtin_amdgcn_s_sleep(10);
-    }
-#endif
     MV_TS(0);
     load(cur, dcur, 0);  // weights first: the longest latency
     // stage this token's Q8_K activation in LDS
@@ -410,14 +404,7 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
     // at a time ahead of the dependent adds), the store
     auto group = [&](const uint4 *c, float d6, int gi) {
         const int gr0 = (group0 + gi) * RL;
-#ifdef MV_LOADONLY
-        uint32_t xx = 0;
-#pragma unroll
-        for (int k = 0; k < CH; k++) xx ^= c[k].x ^ c[k].y ^ c[k].z ^ c[k].w;
-        const float term = (float)(xx & 1u) + d6 + (float)rec[0];
-#else
         const float term = kq_term<KIND>(*(const uint4(*)[CH])c, d6, rec);
-#endif
         MV_TS(2 + 2 * gi);
         if (lane_on) sT[wave][rs * ts + s] = term;
         wave_lds_sync();
