@@ -145,6 +145,8 @@ def load(path=None):
     _sig(lib, "aotk_generate_greedy", i, [vp, sz, sz, C.POINTER(u32)])
     _sig(lib, "aotk_kv_download", i, [vp, sz, fp, fp])
     _sig(lib, "aotk_kv_upload", i, [vp, sz, fp, fp])
+    _sig(lib, "aotk_prefix_save", i, [vp, C.POINTER(u32), sz, sz, vp, sz, C.POINTER(sz)])
+    _sig(lib, "aotk_prefix_load", i, [vp, vp, sz, C.POINTER(u32), sz, C.POINTER(sz), C.POINTER(sz)])
     _sig(lib, "aotk_stream", vp, [])
     _sig(lib, "aotk_time_matvec", i, [C.POINTER(vp), sz, vp, sz, C.POINTER(C.c_float)])
     _lib = lib

@@ -306,6 +306,28 @@ class State:
         v = np.ascontiguousarray(v, np.float32)
         abi.check(_lib().aotk_kv_upload(self.h, n_pos, k.ctypes.data_as(fp), v.ctypes.data_as(fp)))
 
+    def save_prefix(self, tokens, n_cached):
+        """prefix::serialize (prefix.rs:114-141): the AOTP v2 blob of `tokens`
+        with the KV rows of their first n_cached positions."""
+        arr = (C.c_uint32 * max(1, len(tokens)))(*[int(t) for t in tokens])
+        n = C.c_size_t()
+        abi.check(_lib().aotk_prefix_save(self.h, arr, len(tokens), int(n_cached), None, 0, C.byref(n)))
+        out = np.empty(n.value, np.uint8)
+        abi.check(_lib().aotk_prefix_save(self.h, arr, len(tokens), int(n_cached), out.ctypes.data_as(C.c_void_p),
+                                          out.size, C.byref(n)))
+        return out.tobytes()
+
+    def load_prefix(self, blob):
+        """Prefix::parse + load_into (prefix.rs:48-108): returns (tokens, n_cached)."""
+        blob = bytes(blob)
+        buf = np.frombuffer(blob, np.uint8)
+        n, nc = C.c_size_t(), C.c_size_t()
+        ptr = buf.ctypes.data_as(C.c_void_p) if buf.size else None
+        abi.check(_lib().aotk_prefix_load(self.h, ptr, buf.size, None, 0, C.byref(n), C.byref(nc)))
+        toks = (C.c_uint32 * n.value)()
+        abi.check(_lib().aotk_prefix_load(self.h, ptr, buf.size, toks, n.value, C.byref(n), C.byref(nc)))
+        return list(toks), nc.value
+
     def free(self):
         if self.h:
             _lib().aotk_state_free(self.h)

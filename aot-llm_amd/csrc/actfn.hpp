@@ -30,59 +30,74 @@ __device__ __forceinline__ void amax_step(float &amax, int &idx) {
     }
 }
 
+// One lane's share of a Q8_K block (quant.rs:248-283) of 256 values held 4
+// per lane (element 4*lane + k) of a wave: the 4 packed quants, the sum of
+// the lane's quad of 4 lanes (lanes 4j hold bsums[j]) and the block scale d.
+struct Q8KLane {
+    uint32_t packed;
+    int quad_sum;
+    float d;
+};
+__device__ __forceinline__ Q8KLane q8k_lane(const float v[4], int lane) {
+    float amax = 0.0f;
+    int idx = 0x7fffffff;
+    for (int k = 0; k < 4; k++) {
+        float a = fabsf(v[k]);
+        if (a > amax) { amax = a; idx = lane * 4 + k; }
+    }
+    amax_step<DPP_XOR1>(amax, idx);
+    amax_step<DPP_XOR2>(amax, idx);
+    amax_step<DPP_HALF_MIRROR>(amax, idx);
+    amax_step<DPP_MIRROR>(amax, idx);
+    // the four rows of 16 lanes, in index order
+    {
+        float ra = readlane_f(amax, 0);
+        int ri = __builtin_amdgcn_readlane(idx, 0);
+#pragma unroll
+        for (int r = 1; r < 4; r++) {
+            const float oa = readlane_f(amax, 16 * r);
+            const int oi = __builtin_amdgcn_readlane(idx, 16 * r);
+            if (oa > ra || (oa == ra && oi < ri)) {
+                ra = oa;
+                ri = oi;
+            }
+        }
+        amax = ra;
+        idx = ri;
+    }
+    const int src_lane = (idx == 0x7fffffff) ? 0 : idx >> 2, sk = idx & 3;
+    const float c0 = readlane_f(v[0], src_lane), c1 = readlane_f(v[1], src_lane);
+    const float c2 = readlane_f(v[2], src_lane), c3 = readlane_f(v[3], src_lane);
+    float max = sk == 0 ? c0 : (sk == 1 ? c1 : (sk == 2 ? c2 : c3));
+    Q8KLane r;
+    r.packed = 0;
+    int sum = 0;
+    r.d = 0.0f;
+    if (amax != 0.0f) {
+        float iscale = -127.0f / max;
+        for (int k = 0; k < 4; k++) {
+            int t = round_i(iscale * v[k]);
+            t = t > 127 ? 127 : t;
+            r.packed |= (uint32_t)(t & 0xFF) << (8 * k);
+            sum += (int8_t)t;
+        }
+        r.d = 1.0f / iscale;
+    }
+    sum += dppx_i<DPP_XOR1>(sum);
+    sum += dppx_i<DPP_XOR2>(sum);
+    r.quad_sum = sum;
+    return r;
+}
+
 // Quantize 256 values held 4 per lane (element 4*lane + k) of one wave into
 // the Q8_K block `blk` (quant.rs:248-283) and/or the 8 Q8_0 blocks
 // 8*blk .. 8*blk+7 (quant.rs:231-245).
 __device__ __forceinline__ void quant256(const float v[4], int lane, size_t blk, ActQ8K q8k, ActQ8_0 q80) {
     if (q8k.qs) {
-        float amax = 0.0f;
-        int idx = 0x7fffffff;
-        for (int k = 0; k < 4; k++) {
-            float a = fabsf(v[k]);
-            if (a > amax) { amax = a; idx = lane * 4 + k; }
-        }
-        amax_step<DPP_XOR1>(amax, idx);
-        amax_step<DPP_XOR2>(amax, idx);
-        amax_step<DPP_HALF_MIRROR>(amax, idx);
-        amax_step<DPP_MIRROR>(amax, idx);
-        // the four rows of 16 lanes, in index order
-        {
-            float ra = readlane_f(amax, 0);
-            int ri = __builtin_amdgcn_readlane(idx, 0);
-#pragma unroll
-            for (int r = 1; r < 4; r++) {
-                const float oa = readlane_f(amax, 16 * r);
-                const int oi = __builtin_amdgcn_readlane(idx, 16 * r);
-                if (oa > ra || (oa == ra && oi < ri)) {
-                    ra = oa;
-                    ri = oi;
-                }
-            }
-            amax = ra;
-            idx = ri;
-        }
-        const int src_lane = (idx == 0x7fffffff) ? 0 : idx >> 2, sk = idx & 3;
-        const float c0 = readlane_f(v[0], src_lane), c1 = readlane_f(v[1], src_lane);
-        const float c2 = readlane_f(v[2], src_lane), c3 = readlane_f(v[3], src_lane);
-        float max = sk == 0 ? c0 : (sk == 1 ? c1 : (sk == 2 ? c2 : c3));
-        uint32_t packed = 0;
-        int sum = 0;
-        float d = 0.0f;
-        if (amax != 0.0f) {
-            float iscale = -127.0f / max;
-            for (int k = 0; k < 4; k++) {
-                int t = round_i(iscale * v[k]);
-                t = t > 127 ? 127 : t;
-                packed |= (uint32_t)(t & 0xFF) << (8 * k);
-                sum += (int8_t)t;
-            }
-            d = 1.0f / iscale;
-        }
-        ((uint32_t *)(q8k.qs + blk * 256))[lane] = packed;
-        sum += dppx_i<DPP_XOR1>(sum);
-        sum += dppx_i<DPP_XOR2>(sum);
-        if ((lane & 3) == 0) q8k.bsums[blk * 16 + lane / 4] = (int16_t)sum;
-        if (lane == 0) q8k.d[blk] = d;
+        const Q8KLane r = q8k_lane(v, lane);
+        ((uint32_t *)(q8k.qs + blk * 256))[lane] = r.packed;
+        if ((lane & 3) == 0) q8k.bsums[blk * 16 + lane / 4] = (int16_t)r.quad_sum;
+        if (lane == 0) q8k.d[blk] = r.d;
     }
     if (q80.qs) {
         float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));

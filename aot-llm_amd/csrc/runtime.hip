@@ -1097,6 +1097,90 @@ int aotk_kv_upload(aotk_state *st, size_t n_pos, const float *k_host, const floa
     return 0;
 }
 
+// ------------------------------------------------------ KV prefix blobs
+// "AOTP" version 2 (prefix.rs:15-141), little-endian:
+//   0 "AOTP" | 4 version | 8 n_tokens | 12 n_layer | 16 kv_dim | 20 n_cached
+//   24 token ids u32[n_tokens], zero padding to a 64-byte boundary, then per
+//   layer the K rows f32[n_cached * kv_dim] and the V rows likewise.
+// Version 1 blobs carry n_cached = n_tokens.
+static constexpr size_t PREFIX_HEADER = 24;
+
+static size_t prefix_data_off(size_t n_tokens) { return (PREFIX_HEADER + 4 * n_tokens + 63) / 64 * 64; }
+
+static uint32_t le32_at(const uint8_t *b, size_t at) {
+    return (uint32_t)b[at] | ((uint32_t)b[at + 1] << 8) | ((uint32_t)b[at + 2] << 16) | ((uint32_t)b[at + 3] << 24);
+}
+
+static void put_le32(uint8_t *b, size_t at, uint32_t v) {
+    b[at] = (uint8_t)v;
+    b[at + 1] = (uint8_t)(v >> 8);
+    b[at + 2] = (uint8_t)(v >> 16);
+    b[at + 3] = (uint8_t)(v >> 24);
+}
+
+int aotk_prefix_save(aotk_state *st, const uint32_t *tokens, size_t n_tokens, size_t n_cached, void *out, size_t out_cap,
+                     size_t *out_len) {
+    if (!st || !out_len || (n_tokens > 0 && !tokens)) return fail("prefix_save: null argument");
+    const aotk_dims &d = st->m->spec.dims;
+    const size_t kv = d.n_kv_head * d.head_dim;
+    if (n_cached > n_tokens) n_cached = n_tokens;  // serialize: n_cached.min(n)
+    if (n_cached > st->ctx) return fail("prefix_save: %zu cached rows exceed the context %zu", n_cached, st->ctx);
+    const size_t off = prefix_data_off(n_tokens);
+    const size_t rows = n_cached * kv * 4;
+    const size_t len = off + d.n_layer * 2 * rows;
+    *out_len = len;
+    if (!out) return 0;  // size query
+    if (out_cap < len) return fail("prefix_save: buffer of %zu bytes, %zu needed", out_cap, len);
+    uint8_t *b = (uint8_t *)out;
+    memcpy(b, "AOTP", 4);
+    put_le32(b, 4, 2);
+    put_le32(b, 8, (uint32_t)n_tokens);
+    put_le32(b, 12, (uint32_t)d.n_layer);
+    put_le32(b, 16, (uint32_t)kv);
+    put_le32(b, 20, (uint32_t)n_cached);
+    for (size_t i = 0; i < n_tokens; i++) put_le32(b, PREFIX_HEADER + 4 * i, tokens[i]);
+    memset(b + PREFIX_HEADER + 4 * n_tokens, 0, off - PREFIX_HEADER - 4 * n_tokens);
+    // the device holds little-endian f32 like the host: rows copy as bytes
+    for (size_t l = 0; l < d.n_layer && rows > 0; l++) {
+        HIPC(hipMemcpyAsync(b + off + (2 * l) * rows, st->k_cache + l * st->ctx * kv, rows, hipMemcpyDeviceToHost, g_stream));
+        HIPC(hipMemcpyAsync(b + off + (2 * l + 1) * rows, st->v_cache + l * st->ctx * kv, rows, hipMemcpyDeviceToHost, g_stream));
+    }
+    HIPC(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+int aotk_prefix_load(aotk_state *st, const void *blob, size_t len, uint32_t *tokens_out, size_t tokens_cap,
+                     size_t *n_tokens, size_t *n_cached) {
+    if (!st || (!blob && len > 0) || !n_tokens || !n_cached) return fail("prefix_load: null argument");
+    const aotk_dims &d = st->m->spec.dims;
+    const size_t kv = d.n_kv_head * d.head_dim;
+    const uint8_t *b = (const uint8_t *)blob;
+    // Prefix::parse (prefix.rs:48-73): None -> "not a KV cache of this model"
+    if (len < PREFIX_HEADER || memcmp(b, "AOTP", 4) != 0) return fail("prefix_load: not a KV prefix blob");
+    const uint32_t version = le32_at(b, 4);
+    if (version != 1 && version != 2) return fail("prefix_load: unknown version %u", version);
+    const size_t n = le32_at(b, 8), nl = le32_at(b, 12), kvd = le32_at(b, 16);
+    const size_t nc = version == 1 ? n : le32_at(b, 20);
+    if (nl != d.n_layer || kvd != kv || n == 0 || nc > n) return fail("prefix_load: not a KV cache of this model");
+    const size_t off = prefix_data_off(n);
+    const size_t rows = nc * kv * 4;
+    if (len < off + nl * 2 * rows || len < PREFIX_HEADER + 4 * n) return fail("prefix_load: blob truncated");
+    if (nc > st->ctx) return fail("prefix_load: %zu cached rows exceed the context %zu", nc, st->ctx);
+    *n_tokens = n;
+    *n_cached = nc;
+    if (tokens_out) {
+        if (tokens_cap < n) return fail("prefix_load: room for %zu tokens, %zu needed", tokens_cap, n);
+        for (size_t i = 0; i < n; i++) tokens_out[i] = le32_at(b, PREFIX_HEADER + 4 * i);
+    }
+    // load_into (prefix.rs:96-108): positions 0..n_cached of every layer
+    for (size_t l = 0; l < nl && rows > 0; l++) {
+        HIPC(hipMemcpyAsync(st->k_cache + l * st->ctx * kv, b + off + (2 * l) * rows, rows, hipMemcpyHostToDevice, g_stream));
+        HIPC(hipMemcpyAsync(st->v_cache + l * st->ctx * kv, b + off + (2 * l + 1) * rows, rows, hipMemcpyHostToDevice, g_stream));
+    }
+    HIPC(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
 }  // extern "C"
 
 extern "C" {

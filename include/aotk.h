@@ -263,6 +263,21 @@ int aotk_generate_greedy(aotk_state *state, size_t pos, size_t n, uint32_t *toke
  * reference's cache: [n_layer][n_pos][kv_dim] f32 for K, then the same for V. */
 int aotk_kv_download(aotk_state *state, size_t n_pos, float *k_host, float *v_host);
 int aotk_kv_upload(aotk_state *state, size_t n_pos, const float *k_host, const float *v_host);
+/* KV prefix blobs "AOTP" v2 (prefix.rs:15-141; --save-kv / --load-kv and
+ * the baked prefix, app.rs:397-489, 631-632).
+ * aotk_prefix_save replaces prefix::serialize (prefix.rs:114-141): header,
+ * the n_tokens ids, zero padding to 64 bytes, then per layer the K and V rows
+ * of positions [0, min(n_cached, n_tokens)). With out == NULL it only stores
+ * the blob size in *out_len.
+ * aotk_prefix_load replaces Prefix::parse + load_into (prefix.rs:48-108):
+ * the checks of parse (magic, version 1 or 2, n_layer and kv_dim of this
+ * model, n_tokens > 0, n_cached <= n_tokens, length) fail with -1 where the
+ * reference returns None; on success the cached rows go to positions
+ * [0, n_cached) of the device cache and the ids to tokens_out (if given). */
+int aotk_prefix_save(aotk_state *state, const uint32_t *tokens, size_t n_tokens, size_t n_cached, void *out,
+                     size_t out_cap, size_t *out_len);
+int aotk_prefix_load(aotk_state *state, const void *blob, size_t len, uint32_t *tokens_out, size_t tokens_cap,
+                     size_t *n_tokens, size_t *n_cached);
 /* Measurement helper (the reference's #[ignore] bench_ops harness,
  * crates/aot-kernels/tests/metal.rs:459-641): quantizes x_dev once, then
  * launches the matvec of ws[0], ws[1], ... in turn (rotating copies keeps

@@ -229,3 +229,51 @@ class Model:
 def argmax(x):
     x = np.ascontiguousarray(x, np.float32)
     return int(load().or_argmax(ptr(x), x.size))
+
+
+# ----------------------------------------------------------- KV prefix blobs
+# Restatement of crates/aot-kernels/src/prefix.rs (format comment :15-26):
+# "AOTP", version, n_tokens, n_layer, kv_dim, n_cached (u32 LE each), the
+# token ids, zero padding to 64 bytes, then per layer K rows and V rows f32.
+PREFIX_MAGIC = b"AOTP"
+
+
+def prefix_serialize(k_cache, v_cache, ctx, n_layer, kv_dim, tokens, n_cached):
+    """prefix::serialize (prefix.rs:114-141); k_cache / v_cache laid out
+    [n_layer][ctx][kv_dim] like State::k_cache."""
+    n = len(tokens)
+    n_cached = min(n_cached, n)  # :117
+    out = bytearray()
+    out += PREFIX_MAGIC
+    out += np.array([2, n, n_layer, kv_dim, n_cached], "<u4").tobytes()  # :120-125
+    out += np.asarray(tokens, "<u4").tobytes()  # :126-128
+    while len(out) % 64:  # :129-131
+        out.append(0)
+    k = np.asarray(k_cache, "<f4").reshape(n_layer, ctx, kv_dim)
+    v = np.asarray(v_cache, "<f4").reshape(n_layer, ctx, kv_dim)
+    for layer in range(n_layer):  # :132-139
+        out += k[layer, :n_cached].tobytes()
+        out += v[layer, :n_cached].tobytes()
+    return bytes(out)
+
+
+def prefix_parse(blob, n_layer, kv_dim):
+    """Prefix::parse (prefix.rs:48-73): (tokens, n_cached, k_rows, v_rows)
+    with rows [n_layer][n_cached][kv_dim], or None where the reference
+    returns None."""
+    if len(blob) < 24 or blob[:4] != PREFIX_MAGIC:
+        return None
+    version, n, nl, kvd, nc = np.frombuffer(blob[4:24], "<u4").tolist()
+    if version not in (1, 2):
+        return None
+    if version == 1:
+        nc = n
+    if nl != n_layer or kvd != kv_dim or n == 0 or nc > n:
+        return None
+    tokens = np.frombuffer(blob[24:24 + 4 * n], "<u4").tolist()
+    off = (24 + 4 * n + 63) // 64 * 64
+    need = off + nl * 2 * nc * kvd * 4
+    if len(blob) < need:
+        return None
+    data = np.frombuffer(blob[off:need], "<f4").reshape(nl, 2, nc, kvd)
+    return tokens, nc, data[:, 0].copy(), data[:, 1].copy()
