@@ -74,6 +74,12 @@ class ModelSpec(C.Structure):
                 ("output", Tensor), ("rope_freqs", Tensor), ("layers", C.POINTER(Layer))]
 
 
+class SamplerConfig(C.Structure):
+    """aotk_sampler_config (sampler.rs SamplerConfig)."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float), ("repeat_penalty", C.c_float),
+                ("repeat_last_n", C.c_uint32), ("reserved", C.c_uint32), ("seed", C.c_uint64)]
+
+
 assert C.sizeof(Tensor) == 40
 assert C.sizeof(Layer) == 16 * 40 + 8
 
@@ -145,6 +151,11 @@ def load(path=None):
     _sig(lib, "aotk_generate_greedy", i, [vp, sz, sz, C.POINTER(u32)])
     _sig(lib, "aotk_kv_download", i, [vp, sz, fp, fp])
     _sig(lib, "aotk_kv_upload", i, [vp, sz, fp, fp])
+    _sig(lib, "aotk_sampler_new", vp, [C.POINTER(SamplerConfig)])
+    _sig(lib, "aotk_sampler_free", i, [vp])
+    _sig(lib, "aotk_set_logits", i, [vp, fp])
+    _sig(lib, "aotk_sample", i, [vp, vp, C.POINTER(u32), sz, C.POINTER(u32)])
+    _sig(lib, "aotk_generate", i, [vp, vp, sz, sz, C.POINTER(u32), sz, C.POINTER(u32)])
     _sig(lib, "aotk_prefix_save", i, [vp, C.POINTER(u32), sz, sz, vp, sz, C.POINTER(sz)])
     _sig(lib, "aotk_prefix_load", i, [vp, vp, sz, C.POINTER(u32), sz, C.POINTER(sz), C.POINTER(sz)])
     _sig(lib, "aotk_stream", vp, [])

@@ -248,6 +248,31 @@ class Model:
             pass
 
 
+class Sampler:
+    """sampler.rs Sampler on the device: the config and the xorshift64* state
+    (seeded through splitmix) live in the library."""
+
+    def __init__(self, temperature=0.0, top_k=40, top_p=0.95, repeat_penalty=1.0, repeat_last_n=64, seed=42):
+        self.cfg = abi.SamplerConfig(temperature, top_k, top_p, repeat_penalty, repeat_last_n, 0, seed)
+        self.h = abi.check_ptr(_lib().aotk_sampler_new(C.byref(self.cfg)))
+
+    def free(self):
+        if self.h:
+            _lib().aotk_sampler_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _u32_array(xs):
+    xs = [int(x) for x in xs]
+    return (C.c_uint32 * max(1, len(xs)))(*xs), len(xs)
+
+
 class State:
     """Activations + KV cache in HBM for one sequence (state.rs:251-355)."""
 
@@ -305,6 +330,25 @@ class State:
         k = np.ascontiguousarray(k, np.float32)
         v = np.ascontiguousarray(v, np.float32)
         abi.check(_lib().aotk_kv_upload(self.h, n_pos, k.ctypes.data_as(fp), v.ctypes.data_as(fp)))
+
+    def set_logits(self, logits):
+        x = np.ascontiguousarray(logits, np.float32)
+        assert x.size == self.vocab
+        abi.check(_lib().aotk_set_logits(self.h, x.ctypes.data_as(C.POINTER(C.c_float))))
+
+    def sample(self, sampler, recent=()):
+        """Sampler::sample on the current logits (modified in place)."""
+        arr, n = _u32_array(recent)
+        t = C.c_uint32()
+        abi.check(_lib().aotk_sample(self.h, sampler.h, arr, n, C.byref(t)))
+        return t.value
+
+    def generate_sampled(self, sampler, pos, n, recent):
+        """The app.rs:553-610 loop with `sampler`; `recent` = the tokens so far."""
+        arr, nr = _u32_array(recent)
+        out = (C.c_uint32 * n)()
+        abi.check(_lib().aotk_generate(self.h, sampler.h, int(pos), int(n), arr, nr, out))
+        return list(out)
 
     def save_prefix(self, tokens, n_cached):
         """prefix::serialize (prefix.rs:114-141): the AOTP v2 blob of `tokens`

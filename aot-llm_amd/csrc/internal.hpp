@@ -134,6 +134,25 @@ void launch_ref_to_q8_0(const aotk_block_q8_0 *in, size_t n, size_t rows, ActQ8_
 // `add` (may be null) is added to the result (fused residual add).
 void launch_matvec(const DevWeight &w, const void *x_act, size_t m, float *y, const float *add, hipStream_t s);
 // Up to three matrices sharing kind/cols/input in one launch (q/k/v, gate/up).
+// Token sampling (sampler.cpp / sampler.rs); see sampler.hip.
+constexpr int SAMP_KMAX = 1024;   // most candidates after top-k on the device
+constexpr int SAMP_SLICE = 2048;  // logits per block of the first top-k stage
+constexpr int SAMP_MERGE = 8192;  // keys per block of the merge stages
+struct SampleArgs {
+    float *logits;
+    size_t vocab;
+    float temperature, top_p, repeat_penalty;
+    uint32_t repeat_last_n;
+    int k;                // candidates after top-k (temperature > 0)
+    uint64_t *rng;        // xorshift64* state
+    uint32_t *win;        // tokens so far (penalty window source)
+    uint32_t *count;      // entries of win; the pick is appended
+    uint32_t *tok_out;    // the picked token
+    uint64_t *scratch;    // sampler_scratch_bytes(vocab)
+    float *argmax_ws;     // launch_argmax scratch
+};
+size_t sampler_scratch_bytes(size_t vocab);
+void launch_sample(const SampleArgs &p, hipStream_t s);
 void launch_matvec_multi(int n, const DevWeight *const ws[], float *const ys[], const void *x_act, size_t m,
                          hipStream_t s);
 // Matrices of a Q4_K/Q5_K kind (up to three, e.g. q and k) and one Q6_K

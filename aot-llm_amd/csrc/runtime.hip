@@ -735,7 +735,7 @@ struct aotk_state {
     float *attn_ws;
     size_t attn_ws_bytes;
     float *am_ws;
-    uint32_t *ctl;     // [0] token, [1] pos, [2] argmax, [3] generated count
+    uint32_t *ctl;     // [0] token, [1] pos, [2] argmax / sampled, [3] generated count, [4] sampler window count
     uint32_t *tokens;  // [max_batch]
     uint32_t *hist;    // [ctx]
     uint32_t *ctl_host;  // pinned staging for the control words
@@ -744,11 +744,28 @@ struct aotk_state {
     // increment) captured once as a HIP graph; every kernel of it reads the
     // token and the position from `ctl`, so the same graph serves every step.
     hipGraphExec_t gen_exec = nullptr;
+    // Sampling: the token window of the repetition penalty (recent ++
+    // generated), the top-k scratch, and the generation step captured for
+    // one sampler (its config and rng address are baked into the graph).
+    uint32_t *swin = nullptr;  // [ctx + SAMP_WIN_EXTRA]
+    uint64_t *samp_ws = nullptr;
+    hipGraphExec_t samp_exec = nullptr;
+    aotk_sampler_config samp_cfg = {};
+    const void *samp_rng = nullptr;
+};
+
+// Recent tokens the window keeps beyond the context (repeat_last_n cap).
+static constexpr size_t SAMP_WIN_EXTRA = 4096;
+
+struct aotk_sampler {
+    aotk_sampler_config cfg;
+    uint64_t *rng;  // device
 };
 
 static void state_release(aotk_state *st) {
     (void)hipStreamSynchronize(g_stream);
     if (st->gen_exec) (void)hipGraphExecDestroy(st->gen_exec);
+    if (st->samp_exec) (void)hipGraphExecDestroy(st->samp_exec);
     for (void *p : st->allocs) (void)hipFree(p);
     if (st->ctl_host) (void)hipHostFree(st->ctl_host);
     delete st;
@@ -833,7 +850,9 @@ aotk_state *aotk_state_new(aotk_model *m, size_t ctx, size_t max_batch) {
     st->ctl = (uint32_t *)alloc(64);
     st->tokens = (uint32_t *)alloc(B * 4);
     st->hist = (uint32_t *)alloc(ctx * 4);
-    ok = ok && st->attn_ws && st->ctl && st->tokens && st->hist;
+    st->swin = (uint32_t *)alloc((ctx + SAMP_WIN_EXTRA + 1) * 4);
+    st->samp_ws = (uint64_t *)alloc(sampler_scratch_bytes(d.vocab));
+    ok = ok && st->attn_ws && st->ctl && st->tokens && st->hist && st->swin && st->samp_ws;
     if (ok && hipHostMalloc((void **)&st->ctl_host, 64, hipHostMallocDefault) != hipSuccess) ok = false;
     // The tables are copied on the library stream, behind the zero fills
     // queued there by alloc() (that stream does not synchronise with the
@@ -1093,6 +1112,148 @@ int aotk_kv_upload(aotk_state *st, size_t n_pos, const float *k_host, const floa
         HIPC(hipMemcpyAsync(st->k_cache + l * st->ctx * kv, k_host + l * n_pos * kv, n_pos * kv * 4, hipMemcpyHostToDevice, g_stream));
         HIPC(hipMemcpyAsync(st->v_cache + l * st->ctx * kv, v_host + l * n_pos * kv, n_pos * kv * 4, hipMemcpyHostToDevice, g_stream));
     }
+    HIPC(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+// ------------------------------------------------------------- sampling
+static uint64_t splitmix_seed(uint64_t seed) {
+    // sampler.rs:113-118
+    uint64_t z = seed + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return (z ^ (z >> 31)) | 1ull;
+}
+
+aotk_sampler *aotk_sampler_new(const aotk_sampler_config *cfg) {
+    if (ensure_init()) return nullptr;
+    if (!cfg) {
+        fail("sampler_new: null config");
+        return nullptr;
+    }
+    if (cfg->repeat_last_n > SAMP_WIN_EXTRA) {
+        fail("sampler_new: repeat_last_n %u exceeds %zu", cfg->repeat_last_n, SAMP_WIN_EXTRA);
+        return nullptr;
+    }
+    aotk_sampler *sp = new aotk_sampler();
+    sp->cfg = *cfg;
+    const uint64_t r = splitmix_seed(cfg->seed);
+    if (hipMalloc(&sp->rng, 8) != hipSuccess || hipMemcpy(sp->rng, &r, 8, hipMemcpyHostToDevice) != hipSuccess) {
+        fail("sampler_new: device allocation failed");
+        if (sp->rng) (void)hipFree(sp->rng);
+        delete sp;
+        return nullptr;
+    }
+    return sp;
+}
+
+int aotk_sampler_free(aotk_sampler *sp) {
+    if (!sp) return 0;
+    (void)hipStreamSynchronize(g_stream);
+    (void)hipFree(sp->rng);
+    delete sp;
+    return 0;
+}
+
+static int sample_args(aotk_state *st, aotk_sampler *sp, SampleArgs &p) {
+    const aotk_sampler_config &c = sp->cfg;
+    const size_t V = st->m->spec.dims.vocab;
+    const size_t k = c.top_k > 0 ? (c.top_k < V ? c.top_k : V) : V;  // sampler.rs:67
+    if (c.temperature > 0.0f && k > (size_t)SAMP_KMAX)
+        return fail("sampler: %zu candidates after top-k, at most %d on the device", k, SAMP_KMAX);
+    p.logits = st->logits;
+    p.vocab = V;
+    p.temperature = c.temperature;
+    p.top_p = c.top_p;
+    p.repeat_penalty = c.repeat_penalty;
+    p.repeat_last_n = c.repeat_last_n;
+    p.k = (int)k;
+    p.rng = sp->rng;
+    p.win = st->swin;
+    p.count = st->ctl + 4;
+    p.tok_out = st->ctl + 2;
+    p.scratch = st->samp_ws;
+    p.argmax_ws = st->am_ws;
+    return 0;
+}
+
+// The window starts as the last repeat_last_n tokens of `recent`.
+static int upload_window(aotk_state *st, aotk_sampler *sp, const uint32_t *recent, size_t n_recent) {
+    const size_t w = n_recent < sp->cfg.repeat_last_n ? n_recent : sp->cfg.repeat_last_n;
+    if (w > 0) {
+        if (!recent) return fail("sampler: null recent tokens");
+        HIPC(hipMemcpyAsync(st->swin, recent + (n_recent - w), w * 4, hipMemcpyHostToDevice, g_stream));
+    }
+    st->ctl_host[4] = (uint32_t)w;
+    HIPC(hipMemcpyAsync(st->ctl + 4, st->ctl_host + 4, 4, hipMemcpyHostToDevice, g_stream));
+    return 0;
+}
+
+int aotk_set_logits(aotk_state *st, const float *logits_host) {
+    if (!st || !logits_host) return fail("set_logits: null argument");
+    HIPC(hipMemcpyAsync(st->logits, logits_host, st->m->spec.dims.vocab * 4, hipMemcpyHostToDevice, g_stream));
+    HIPC(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+int aotk_sample(aotk_state *st, aotk_sampler *sp, const uint32_t *recent, size_t n_recent, uint32_t *token_out) {
+    if (!st || !sp || !token_out) return fail("sample: null argument");
+    SampleArgs p;
+    if (sample_args(st, sp, p) || upload_window(st, sp, recent, n_recent)) return -1;
+    launch_sample(p, g_stream);
+    HIPC(hipGetLastError());
+    HIPC(hipMemcpyAsync(st->ctl_host + 2, st->ctl + 2, 4, hipMemcpyDeviceToHost, g_stream));
+    HIPC(hipStreamSynchronize(g_stream));
+    *token_out = st->ctl_host[2];
+    return 0;
+}
+
+int aotk_generate(aotk_state *st, aotk_sampler *sp, size_t pos, size_t n, const uint32_t *recent, size_t n_recent,
+                  uint32_t *tokens_out) {
+    if (!st || !sp || (n > 0 && !tokens_out)) return fail("generate: null argument");
+    if (n == 0) return 0;
+    if (pos + n - 1 > st->ctx) return fail("generation of %zu tokens from %zu exceeds the context %zu", n, pos, st->ctx);
+    SampleArgs p;
+    if (sample_args(st, sp, p) || upload_window(st, sp, recent, n_recent)) return -1;
+    st->ctl_host[1] = (uint32_t)pos;
+    st->ctl_host[3] = 0;
+    HIPC(hipMemcpyAsync(st->ctl + 1, st->ctl_host + 1, 4, hipMemcpyHostToDevice, g_stream));
+    HIPC(hipMemcpyAsync(st->ctl + 3, st->ctl_host + 3, 4, hipMemcpyHostToDevice, g_stream));
+    auto pick = [&]() {
+        launch_sample(p, g_stream);
+        launch_advance(st->ctl, (int *)(st->ctl + 3), st->hist, st->ctl + 2, g_stream);
+    };
+    auto step = [&]() {
+        pick();
+        run_decode_step(st, 1);
+        launch_inc((int *)(st->ctl + 1), g_stream);
+    };
+    // the captured step bakes in the sampler's config and rng address
+    const bool same = st->samp_exec && st->samp_rng == (const void *)sp->rng &&
+                      memcmp(&st->samp_cfg, &sp->cfg, sizeof(sp->cfg)) == 0;
+    if (n > 1 && !same && !getenv("AOTK_NO_GRAPH")) {
+        if (st->samp_exec) (void)hipGraphExecDestroy(st->samp_exec);
+        st->samp_exec = nullptr;
+        hipGraph_t graph = nullptr;
+        HIPC(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal));
+        step();
+        hipError_t e = hipStreamEndCapture(g_stream, &graph);
+        if (e == hipSuccess) e = hipGraphInstantiate(&st->samp_exec, graph, nullptr, nullptr, 0);
+        if (graph) (void)hipGraphDestroy(graph);
+        if (e != hipSuccess) {
+            st->samp_exec = nullptr;
+            return fail("graph capture of the sampling step failed: %s", hipGetErrorString(e));
+        }
+        st->samp_cfg = sp->cfg;
+        st->samp_rng = sp->rng;
+    }
+    for (size_t g = 0; g + 1 < n; g++) {
+        if (st->samp_exec) HIPC(hipGraphLaunch(st->samp_exec, g_stream));
+        else step();
+    }
+    pick();
+    HIPC(hipGetLastError());
+    HIPC(hipMemcpyAsync(tokens_out, st->hist, n * 4, hipMemcpyDeviceToHost, g_stream));
     HIPC(hipStreamSynchronize(g_stream));
     return 0;
 }

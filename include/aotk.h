@@ -263,6 +263,40 @@ int aotk_generate_greedy(aotk_state *state, size_t pos, size_t n, uint32_t *toke
  * reference's cache: [n_layer][n_pos][kv_dim] f32 for K, then the same for V. */
 int aotk_kv_download(aotk_state *state, size_t n_pos, float *k_host, float *v_host);
 int aotk_kv_upload(aotk_state *state, size_t n_pos, const float *k_host, const float *v_host);
+/* Stochastic sampler (sampler.rs:1-114): SamplerConfig field for field
+ * (temperature <= 0 selects the arg-max; top_k 0 disables top-k; top_p 1
+ * and repeat_penalty 1 disable those) and the xorshift64* stream seeded
+ * through splitmix (sampler.rs:32-45, 113-118), kept in device memory.
+ * On the device the candidate count min(top_k, vocab) (vocab when top_k is
+ * 0) must be at most 1024 when temperature > 0. Candidates of equal scaled
+ * logit are ordered by ascending token id (the reference's unstable sort
+ * leaves that order open). */
+typedef struct aotk_sampler_config {
+    float temperature;
+    uint32_t top_k;
+    float top_p;
+    float repeat_penalty;
+    uint32_t repeat_last_n;
+    uint32_t reserved;
+    uint64_t seed;
+} aotk_sampler_config;
+typedef struct aotk_sampler aotk_sampler;
+aotk_sampler *aotk_sampler_new(const aotk_sampler_config *cfg);
+int aotk_sampler_free(aotk_sampler *sampler);
+/* Sampler::sample on the state's current logits (modified in place by the
+ * repetition penalty, sampler.rs:53-60), `recent` = the tokens so far
+ * (the last repeat_last_n are penalised). */
+int aotk_sample(aotk_state *state, aotk_sampler *sampler, const uint32_t *recent, size_t n_recent, uint32_t *token_out);
+/* Replace the state's vocab logits (the `logits: &mut [f32]` argument of
+ * Sampler::sample, sampler.rs:49) with a host array. */
+int aotk_set_logits(aotk_state *state, const float *logits_host);
+/* The generation loop of app.rs:553-610 with a sampler: from the current
+ * logits, n tokens at positions pos, pos+1, ... (each fed back except the
+ * last), the penalty window running over recent ++ generated. Device-resident
+ * like aotk_generate_greedy. */
+int aotk_generate(aotk_state *state, aotk_sampler *sampler, size_t pos, size_t n, const uint32_t *recent, size_t n_recent,
+                  uint32_t *tokens_out);
+
 /* KV prefix blobs "AOTP" v2 (prefix.rs:15-141; --save-kv / --load-kv and
  * the baked prefix, app.rs:397-489, 631-632).
  * aotk_prefix_save replaces prefix::serialize (prefix.rs:114-141): header,

@@ -1352,6 +1352,102 @@ uint32_t or_argmax(const float *x, size_t n) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Sampler (sampler.rs)                                                     */
+/* ------------------------------------------------------------------------ */
+
+uint64_t or_sampler_seed(uint64_t seed) {
+    /* splitmix (sampler.rs:113-118), forced odd */
+    uint64_t z = seed + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return (z ^ (z >> 31)) | 1ull;
+}
+
+static float or_next_f32(uint64_t *rng) {
+    /* xorshift64* (sampler.rs:38-45) */
+    uint64_t r = *rng;
+    r ^= r >> 12;
+    r ^= r << 25;
+    r ^= r >> 27;
+    *rng = r;
+    uint64_t v = r * 0x2545F4914F6CDD1Dull;
+    return (float)(v >> 40) / (float)(1ull << 24);
+}
+
+typedef struct {
+    float v;
+    uint32_t i;
+} or_cand;
+
+/* f32::total_cmp order as an unsigned key (-NaN < -inf < ... < -0 < +0 < ... < +NaN) */
+static uint32_t or_total_key(float f) {
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+static int or_cand_desc(const void *pa, const void *pb) {
+    const or_cand *a = (const or_cand *)pa, *b = (const or_cand *)pb;
+    uint32_t ka = or_total_key(a->v), kb = or_total_key(b->v);
+    if (ka != kb) return ka > kb ? -1 : 1;
+    return a->i < b->i ? -1 : (a->i > b->i ? 1 : 0);
+}
+
+uint32_t or_sample(const aotk_sampler_config *cfg, uint64_t *rng, float *logits, size_t n, const uint32_t *recent,
+                   size_t n_recent) {
+    /* repetition penalty (sampler.rs:53-60) */
+    if (cfg->repeat_penalty != 1.0f && cfg->repeat_last_n > 0) {
+        size_t start = n_recent > cfg->repeat_last_n ? n_recent - cfg->repeat_last_n : 0;
+        for (size_t j = start; j < n_recent; j++) {
+            float *l = &logits[recent[j]];
+            *l = *l > 0.0f ? *l / cfg->repeat_penalty : *l * cfg->repeat_penalty;
+        }
+    }
+    if (cfg->temperature <= 0.0f) return or_argmax(logits, n); /* :61-63 */
+    const float inv_t = 1.0f / cfg->temperature;
+    or_cand *c = (or_cand *)malloc(n * sizeof(or_cand));
+    for (size_t i = 0; i < n; i++) {
+        c[i].v = logits[i] * inv_t;
+        c[i].i = (uint32_t)i;
+    }
+    size_t k = cfg->top_k > 0 ? (cfg->top_k < n ? cfg->top_k : n) : n; /* :67 */
+    /* select the k largest, then sort them descending (:68-74): one sort
+       gives the same k in the same order */
+    qsort(c, n, sizeof(or_cand), or_cand_desc);
+    const float max = c[0].v;
+    float sum = 0.0f;
+    for (size_t i = 0; i < k; i++) { /* :75-80 */
+        c[i].v = expf(c[i].v - max);
+        sum += c[i].v;
+    }
+    size_t nn = k;
+    if (cfg->top_p < 1.0f) { /* :81-91 */
+        float acc = 0.0f;
+        for (size_t i = 0; i < k; i++) {
+            acc += c[i].v / sum;
+            if (acc >= cfg->top_p) {
+                nn = i + 1;
+                break;
+            }
+        }
+        sum = 0.0f;
+        for (size_t i = 0; i < nn; i++) sum += c[i].v;
+    }
+    const float r = or_next_f32(rng) * sum; /* :92-100 */
+    float acc = 0.0f;
+    uint32_t tok = c[nn - 1].i;
+    for (size_t i = 0; i < nn; i++) {
+        acc += c[i].v;
+        if (acc >= r) {
+            tok = c[i].i;
+            break;
+        }
+    }
+    free(c);
+    return tok;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Synthetic weights                                                        */
 /* ------------------------------------------------------------------------ */
 

@@ -98,6 +98,11 @@ void or_attention(or_pool *p, float *out, const float *q, const float *k_cache, 
                   size_t pos0, size_t m, size_t window);
 void or_inv_freq(float *out, size_t rot_dim, float base, const float *factors);
 uint32_t or_argmax(const float *x, size_t n);
+/* sampler.rs: splitmix seeding (:113-118) and Sampler::sample (:47-96) with
+ * the rng state in *rng; ties of equal scaled logits in ascending id order. */
+uint64_t or_sampler_seed(uint64_t seed);
+uint32_t or_sample(const aotk_sampler_config *cfg, uint64_t *rng, float *logits, size_t n, const uint32_t *recent,
+                   size_t n_recent);
 
 /* Synthetic weights: tests and the bench build their models from this
  * generator (shared definition with the product's device generator). */

@@ -58,6 +58,8 @@ def load():
     sig("or_gelu", f, [f])
     sig("or_gelu_mul", None, [vp, vp, sz])
     sig("or_window_start", sz, [sz, sz])
+    sig("or_sampler_seed", u64, [u64])
+    sig("or_sample", u32, [vp, C.POINTER(u64), vp, sz, vp, sz])
     sig("or_attention", None, [vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, sz, sz, sz])
     sig("or_inv_freq", None, [vp, sz, f, vp])
     sig("or_argmax", u32, [vp, sz])
@@ -214,6 +216,21 @@ class Model:
                 pos += 1
         return out
 
+    def generate_sampled(self, pos, n, sampler, recent):
+        """The app.rs:553-610 loop with a sampler: `recent` = the tokens so
+        far (prompt), extended by every sampled token."""
+        all_toks = list(recent)
+        out = []
+        for g in range(n):
+            lg = self.logits()
+            t = sampler.sample(lg, all_toks)
+            out.append(t)
+            all_toks.append(t)
+            if g + 1 < n:
+                self.forward(t, pos, True)
+                pos += 1
+        return out
+
     def close(self):
         if self.m:
             load().or_model_free(self.m)
@@ -229,6 +246,27 @@ class Model:
 def argmax(x):
     x = np.ascontiguousarray(x, np.float32)
     return int(load().or_argmax(ptr(x), x.size))
+
+
+class SamplerConfig(C.Structure):
+    """aotk_sampler_config / sampler.rs SamplerConfig."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float), ("repeat_penalty", C.c_float),
+                ("repeat_last_n", C.c_uint32), ("reserved", C.c_uint32), ("seed", C.c_uint64)]
+
+
+class Sampler:
+    """sampler.rs Sampler: the config and the xorshift64* state."""
+
+    def __init__(self, temperature=0.0, top_k=40, top_p=0.95, repeat_penalty=1.0, repeat_last_n=64, seed=42):
+        self.cfg = SamplerConfig(temperature, top_k, top_p, repeat_penalty, repeat_last_n, 0, seed)
+        self.rng = C.c_uint64(load().or_sampler_seed(seed))
+
+    def sample(self, logits, recent=()):
+        """Sampler::sample; `logits` (float32 array) is modified in place."""
+        assert logits.dtype == np.float32 and logits.flags.c_contiguous
+        rec = np.ascontiguousarray(np.asarray(recent, np.uint32))
+        return int(load().or_sample(C.byref(self.cfg), C.byref(self.rng), ptr(logits), logits.size,
+                                    ptr(rec) if rec.size else None, rec.size))
 
 
 # ----------------------------------------------------------- KV prefix blobs
