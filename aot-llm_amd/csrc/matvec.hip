@@ -535,6 +535,108 @@ __device__ __forceinline__ void mm_load(MmW<KIND> &w, const uint8_t *rowp, const
     }
 }
 
+// One super-block of the 16 rows of a wave for its tiles of 16 tokens:
+// the B fragments are unpacked once, then per tile the exact integer dots
+// (v_mfma_i32_16x16x32_i8), the scale products and the f32 term of the
+// matvec fold (matvec.rs:82-167 per token): term_out[t][i] belongs to
+// token 16t + 4q + i of the lane's row. ys: the tiles' activation rows of
+// this super-block (MM_YS bytes per token); yds: their Q8_K scales.
+template <int KIND, int TT>
+__device__ __forceinline__ void mm_sb_terms(const MmW<KIND> &cur, const uint8_t *ys, const float *yds, int q, int r16,
+                                            int mt, float (&term_out)[TT][4]) {
+    // the lane row's scales (and mins) of this super-block
+    int sc[16], mn[8];
+    if (KIND == AOTK_Q6_K) {
+        const uint32_t scw[4] = {cur.hdr.x, cur.hdr.y, cur.hdr.z, cur.hdr.w};
+#pragma unroll
+        for (int g = 0; g < 16; g++) sc[g] = (int)(int8_t)((scw[g >> 2] >> (8 * (g & 3))) & 0xFFu);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) scale_min_k4(j, cur.hdr.y, cur.hdr.z, cur.hdr.w, sc[j], mn[j]);
+    }
+    // B fragments (the lane's 8 values of each 32-value step j), shared
+    // by the block's token tiles
+    long bq[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        uint32_t w0, w1;
+        if (KIND == AOTK_Q6_K) {
+            const uint2 lo = j < 4 ? cur.q[j] : cur.q2[j - 4];
+            const int quarter = j & 3, sh = 2 * quarter;
+            const uint32_t n0 = quarter >= 2 ? (lo.x >> 4) & 0x0F0F0F0Fu : lo.x & 0x0F0F0F0Fu;
+            const uint32_t n1 = quarter >= 2 ? (lo.y >> 4) & 0x0F0F0F0Fu : lo.y & 0x0F0F0F0Fu;
+            const uint32_t v0 = n0 | (((cur.h6[j].x >> sh) & 0x03030303u) << 4);
+            const uint32_t v1 = n1 | (((cur.h6[j].y >> sh) & 0x03030303u) << 4);
+            // q - 32 per byte (values 0..63, no borrow between bytes)
+            w0 = (v0 | 0x80808080u) - 0x20202020u;
+            w0 ^= 0x80808080u;
+            w1 = (v1 | 0x80808080u) - 0x20202020u;
+            w1 ^= 0x80808080u;
+        } else {
+            const uint2 qb = cur.q[j >> 1];
+            const int hi = j & 1;
+            w0 = hi ? (qb.x >> 4) & 0x0F0F0F0Fu : qb.x & 0x0F0F0F0Fu;
+            w1 = hi ? (qb.y >> 4) & 0x0F0F0F0Fu : qb.y & 0x0F0F0F0Fu;
+            if (KIND == AOTK_Q5_K) {
+                const uint2 hb = cur.q2[j >> 1];
+                w0 |= ((hb.x >> j) & 0x01010101u) << 4;
+                w1 |= ((hb.y >> j) & 0x01010101u) << 4;
+            }
+        }
+        bq[j] = (long)(((unsigned long)w1 << 32) | w0);
+    }
+    long mb[8];
+    if (KIND != AOTK_Q6_K)
+#pragma unroll
+        for (int j = 0; j < 8; j++) mb[j] = (long)(0x0101010101010101ULL * (unsigned long)mn[j]);
+    float dd = 0.0f, dm = 0.0f;
+    if (KIND == AOTK_Q6_K) {
+        dd = cur.d6;
+    } else {
+        dd = f16_to_f32(cur.hdr.x & 0xFFFFu);
+        dm = f16_to_f32(cur.hdr.x >> 16);
+    }
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+        if (16 * t >= mt) break;
+        // A fragments: token 16t + r16, k = 32j + 8q .. +8
+        const uint8_t *yrow = ys + (16 * t + r16) * MM_YS + 8 * q;
+        int sumi[4] = {0, 0, 0, 0};
+        mm_v4i csum = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const long av = *(const long *)(yrow + 32 * j);
+            if (KIND == AOTK_Q6_K) {
+                // two 16-value scale groups per step: lanes q < 2 hold group 2j, q >= 2 group 2j+1
+                const long b_lo = q < 2 ? bq[j] : 0, b_hi = q < 2 ? 0 : bq[j];
+                mm_v4i c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
+                c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b_lo, c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b_hi, c1, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) sumi[i] += __mul24(sc[2 * j], c0[i]) + __mul24(sc[2 * j + 1], c1[i]);
+            } else {
+                mm_v4i c = {0, 0, 0, 0};
+                c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bq[j], c, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) sumi[i] += __mul24(sc[j], c[i]);
+                csum = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, mb[j], csum, 0, 0, 0);
+            }
+        }
+        // the terms of tokens 16t + 4q + i of the lane's row
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float yd = yds[16 * t + 4 * q + i];
+            float term;
+            if (KIND == AOTK_Q6_K) {
+                term = (dd * yd) * (float)sumi[i];
+            } else {
+                term = (dd * yd) * (float)sumi[i] - (dm * yd) * (float)csum[i];
+            }
+            term_out[t][i] = term;
+        }
+    }
+}
+
 template <int KIND, int TT>
 __global__ __launch_bounds__(256) void k_mm_kq(MvArgs a, int m) {
     constexpr int NT = 16 * TT;  // tokens per block
@@ -600,98 +702,13 @@ __global__ __launch_bounds__(256) void k_mm_kq(MvArgs a, int m) {
             mm_load<KIND>(nx2, rowp, drow, sb + 2, nb, q);
             stage_load(r0, sb + 2);
         }
-        // the lane row's scales (and mins) of this super-block
-        int sc[16], mn[8];
-        if (KIND == AOTK_Q6_K) {
-            const uint32_t scw[4] = {cur.hdr.x, cur.hdr.y, cur.hdr.z, cur.hdr.w};
+        float term[TT][4];
+        mm_sb_terms<KIND, TT>(cur, sY[buf], sD[buf], q, r16, mt, term);
 #pragma unroll
-            for (int g = 0; g < 16; g++) sc[g] = (int)(int8_t)((scw[g >> 2] >> (8 * (g & 3))) & 0xFFu);
-        } else {
+        for (int t = 0; t < TT; t++)
 #pragma unroll
-            for (int j = 0; j < 8; j++) scale_min_k4(j, cur.hdr.y, cur.hdr.z, cur.hdr.w, sc[j], mn[j]);
-        }
-        // B fragments (the lane's 8 values of each 32-value step j), shared
-        // by the block's token tiles
-        long bq[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            uint32_t w0, w1;
-            if (KIND == AOTK_Q6_K) {
-                const uint2 lo = j < 4 ? cur.q[j] : cur.q2[j - 4];
-                const int quarter = j & 3, sh = 2 * quarter;
-                const uint32_t n0 = quarter >= 2 ? (lo.x >> 4) & 0x0F0F0F0Fu : lo.x & 0x0F0F0F0Fu;
-                const uint32_t n1 = quarter >= 2 ? (lo.y >> 4) & 0x0F0F0F0Fu : lo.y & 0x0F0F0F0Fu;
-                const uint32_t v0 = n0 | (((cur.h6[j].x >> sh) & 0x03030303u) << 4);
-                const uint32_t v1 = n1 | (((cur.h6[j].y >> sh) & 0x03030303u) << 4);
-                // q - 32 per byte (values 0..63, no borrow between bytes)
-                w0 = (v0 | 0x80808080u) - 0x20202020u;
-                w0 ^= 0x80808080u;
-                w1 = (v1 | 0x80808080u) - 0x20202020u;
-                w1 ^= 0x80808080u;
-            } else {
-                const uint2 qb = cur.q[j >> 1];
-                const int hi = j & 1;
-                w0 = hi ? (qb.x >> 4) & 0x0F0F0F0Fu : qb.x & 0x0F0F0F0Fu;
-                w1 = hi ? (qb.y >> 4) & 0x0F0F0F0Fu : qb.y & 0x0F0F0F0Fu;
-                if (KIND == AOTK_Q5_K) {
-                    const uint2 hb = cur.q2[j >> 1];
-                    w0 |= ((hb.x >> j) & 0x01010101u) << 4;
-                    w1 |= ((hb.y >> j) & 0x01010101u) << 4;
-                }
-            }
-            bq[j] = (long)(((unsigned long)w1 << 32) | w0);
-        }
-        long mb[8];
-        if (KIND != AOTK_Q6_K)
-#pragma unroll
-            for (int j = 0; j < 8; j++) mb[j] = (long)(0x0101010101010101ULL * (unsigned long)mn[j]);
-        float dd = 0.0f, dm = 0.0f;
-        if (KIND == AOTK_Q6_K) {
-            dd = cur.d6;
-        } else {
-            dd = f16_to_f32(cur.hdr.x & 0xFFFFu);
-            dm = f16_to_f32(cur.hdr.x >> 16);
-        }
-        const uint8_t *ys = sY[buf];
-#pragma unroll
-        for (int t = 0; t < TT; t++) {
-            if (16 * t >= mt) break;
-            // A fragments: token 16t + r16, k = 32j + 8q .. +8
-            const uint8_t *yrow = ys + (16 * t + r16) * MM_YS + 8 * q;
-            int sumi[4] = {0, 0, 0, 0};
-            mm_v4i csum = {0, 0, 0, 0};
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const long av = *(const long *)(yrow + 32 * j);
-                if (KIND == AOTK_Q6_K) {
-                    // two 16-value scale groups per step: lanes q < 2 hold group 2j, q >= 2 group 2j+1
-                    const long b_lo = q < 2 ? bq[j] : 0, b_hi = q < 2 ? 0 : bq[j];
-                    mm_v4i c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
-                    c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b_lo, c0, 0, 0, 0);
-                    c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b_hi, c1, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) sumi[i] += __mul24(sc[2 * j], c0[i]) + __mul24(sc[2 * j + 1], c1[i]);
-                } else {
-                    mm_v4i c = {0, 0, 0, 0};
-                    c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bq[j], c, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) sumi[i] += __mul24(sc[j], c[i]);
-                    csum = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, mb[j], csum, 0, 0, 0);
-                }
-            }
-            // fold: tokens 16t + 4q + i of the lane's row
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float yd = sD[buf][16 * t + 4 * q + i];
-                float term;
-                if (KIND == AOTK_Q6_K) {
-                    term = (dd * yd) * (float)sumi[i];
-                } else {
-                    term = (dd * yd) * (float)sumi[i] - (dm * yd) * (float)csum[i];
-                }
-                acc[t][i] = acc[t][i] + term;
-            }
-        }
+            for (int i = 0; i < 4; i++)
+                if (16 * t < mt) acc[t][i] = acc[t][i] + term[t][i];
         if (sb + 1 < nb) stage_store(r1, (sb + 1) % 3);
         __syncthreads();
         cur = nxt;
