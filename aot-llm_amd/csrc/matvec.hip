@@ -726,6 +726,105 @@ __global__ __launch_bounds__(256) void k_mm_kq(MvArgs a, int m) {
     }
 }
 
+// Prompt matmul for matrices of few rows (the grid of k_mm_kq would leave
+// CUs idle): the 4 waves of a block share 16 rows and 16*TT tokens and take
+// the super-blocks in turn (wave w: w, w + 4, ...), each staging its
+// super-block's activations in its own LDS buffers (the next one two steps
+// ahead in registers). After every round of 4 super-blocks the terms meet in
+// LDS and wave t adds tile t's in super-block order, so the fold is the
+// matvec's (bit-identical to m matvecs) while each wave's dependent chain is
+// nb/4 super-blocks long and the grid has 4x the waves.
+template <int KIND, int TT>
+__global__ __launch_bounds__(256) void k_mm_ks(MvArgs a, int m) {
+    constexpr int NT = 16 * TT;
+    constexpr int SV = NT / 4;  // uint4 per lane of one super-block's staging
+    __shared__ __align__(16) uint8_t sY[4][2][NT * MM_YS];
+    __shared__ float sD[4][2][NT];
+    __shared__ float sT[2][4][TT][4][64];  // [round parity][slot][tile][i][lane]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, r16 = lane & 15;
+    const int nb = a.nb;
+    const int grow = blockIdx.x * 16 + r16;
+    const int tok0 = blockIdx.y * NT;
+    const int mt = min(NT, m - tok0);
+    const bool row_ok = grow < a.total_rows;
+    int local;
+    const int sg = seg_of(a, row_ok ? grow : 0, local);
+    const uint8_t *rowp = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * nb * KqGeom<KIND>::RB;
+    const uint16_t *drow = KIND == AOTK_Q6_K ? (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb : nullptr;
+    struct Stg {
+        uint4 v[SV];
+        float d;
+    };
+    auto stage_load = [&](Stg &r, int sb) {
+#pragma unroll
+        for (int k = 0; k < SV; k++) {
+            const int idx = lane + 64 * k;  // NT tokens x 16 uint4
+            const int tk = idx >> 4, c = idx & 15;
+            r.v[k] = tk < mt ? *(const uint4 *)(a.xq + (size_t)(tok0 + tk) * a.cols + (size_t)sb * 256 + 16 * c) : make_uint4(0, 0, 0, 0);
+        }
+        r.d = lane < mt ? a.xd[(size_t)(tok0 + lane) * nb + sb] : 0.0f;
+    };
+    auto stage_store = [&](const Stg &r, int buf) {
+#pragma unroll
+        for (int k = 0; k < SV; k++) {
+            const int idx = lane + 64 * k;
+            *(uint4 *)(sY[wave][buf] + (idx >> 4) * MM_YS + 16 * (idx & 15)) = r.v[k];
+        }
+        if (lane < NT) sD[wave][buf][lane] = r.d;
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // waves < TT: tile `wave`
+    const int rounds = (nb + 3) / 4;
+    MmW<KIND> cur, nxt;
+    Stg r1;
+    if (wave < nb) {
+        mm_load<KIND>(cur, rowp, drow, wave, nb, q);
+        Stg r0;
+        stage_load(r0, wave);
+        stage_store(r0, 0);
+        if (wave + 4 < nb) {
+            mm_load<KIND>(nxt, rowp, drow, wave + 4, nb, q);
+            stage_load(r1, wave + 4);
+        }
+    }
+    wave_lds_sync();
+    for (int r = 0; r < rounds; r++) {
+        const int sb = 4 * r + wave;
+        if (sb < nb) {
+            const int buf = r & 1;
+            float term[TT][4];
+            mm_sb_terms<KIND, TT>(cur, sY[wave][buf], sD[wave][buf], q, r16, mt, term);
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) sT[r & 1][wave][t][i][lane] = term[t][i];
+            if (sb + 4 < nb) {
+                stage_store(r1, buf ^ 1);
+                cur = nxt;
+                if (sb + 8 < nb) {
+                    mm_load<KIND>(nxt, rowp, drow, sb + 8, nb, q);
+                    stage_load(r1, sb + 8);
+                }
+            }
+        }
+        __syncthreads();
+        if (wave < TT) {
+            const int n = min(4, nb - 4 * r);
+            for (int slot = 0; slot < n; slot++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i] = acc[i] + sT[r & 1][slot][wave][i][lane];
+        }
+    }
+    if (wave < TT && row_ok) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int tk = 16 * wave + 4 * q + i;
+            if (tk < mt) store_row(a, grow, tok0 + tk, acc[i]);
+        }
+    }
+}
+
 // ------------------------------------------------------ Q8_0 / Q4_0 / Q5_0
 // Wave = 8 rows. Phase A: lanes turn 32 blocks of 2 rows per pass into the 8
 // per-lane integer sums P and the scale D = f16(d) * y.d, staged in LDS.
@@ -1059,6 +1158,19 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
         // grid reaches 512 blocks (small matrices) or one tile is left
         const unsigned rb = (unsigned)((a.total_rows + 63) / 64);
         const int tiles = (int)((m + 15) / 16);
+        // few rows (measured: 1024-row v at 64 tokens 2x faster, 4096-row
+        // Q6_K down slightly faster, 4096-row Q4_K wo slightly slower):
+        // super-blocks split over the waves
+        const unsigned cells = rb * (unsigned)tiles;
+        if (cells < 128 || (cells <= 256 && a.nb >= 32)) {
+            dim3 gk((unsigned)((a.total_rows + 15) / 16), (unsigned)tiles);
+            switch (kind) {
+            case AOTK_Q4_K: k_mm_ks<AOTK_Q4_K, 1><<<gk, 256, 0, s>>>(a, (int)m); break;
+            case AOTK_Q5_K: k_mm_ks<AOTK_Q5_K, 1><<<gk, 256, 0, s>>>(a, (int)m); break;
+            default: k_mm_ks<AOTK_Q6_K, 1><<<gk, 256, 0, s>>>(a, (int)m); break;
+            }
+            return;
+        }
         int tt = tiles;
         while (tt > 1 && rb * (unsigned)((tiles + tt - 1) / tt) < 512) tt = (tt + 1) / 2;
         dim3 g(rb, (unsigned)((tiles + tt - 1) / tt));
