@@ -258,11 +258,13 @@ __device__ __forceinline__ float exact_seq_sum_t(const float *pp, int n, SeqScra
                 last_g = g[i];
             }
     }
+    SEQ_TS(5);
     if (act) {
         S.e_first[tid] = len > 0 ? ec[0] : SEQ_SINGLE;
         S.e_last[tid] = len > 0 ? last_e : SEQ_SINGLE;
     }
     __syncthreads();
+    SEQ_TS(6);
     int cv = 0, cc = 0, total = 0, after_e = SEQ_SINGLE;
     bool cont = false;
     int v = 0, f = 1, c = 0;
@@ -286,6 +288,7 @@ __device__ __forceinline__ float exact_seq_sum_t(const float *pp, int n, SeqScra
             f = 1;
         }
         wave_scan_seg(v, f, c);
+        SEQ_TS(7);
         if (lane == 63) {
             S.wv[wave] = v;
             S.wf[wave] = f;
