@@ -472,7 +472,7 @@ __global__ __launch_bounds__(576) void k_attn_qk_decode(AttnArgs a, QkvPost p) {
 #endif
 constexpr int ATT_MAX_SPAN = 16384;
 constexpr int SV_DB = 32;         // dims per block
-constexpr int SV_CP = 240;        // positions per chunk
+constexpr int SV_CP = 192;        // positions per chunk
 constexpr int SV_RS = SV_CP + 4;  // floats per dim row of the product buffer
 constexpr int SV_BUF = SV_DB * SV_RS;  // floats per product buffer
 constexpr int SV_SEQ_MIN = 2048;  // shorter spans are summed by one thread
@@ -481,8 +481,8 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     constexpr int DB = SV_DB;
     constexpr int CP = SV_CP;
     __shared__ __align__(16) float e[ATT_MAX_SPAN + 64];
-    // product buffers (+32 floats read past the end by the last group) / sum scratch
-    __shared__ __align__(16) uint8_t ubuf[sizeof(SeqScratch) > (2 * SV_BUF + 32) * 4 ? sizeof(SeqScratch) : (2 * SV_BUF + 32) * 4];
+    // product buffers (+64 floats read past the end by the last groups) / sum scratch
+    __shared__ __align__(16) uint8_t ubuf[sizeof(SeqScratch) > (2 * SV_BUF + 64) * 4 ? sizeof(SeqScratch) : (2 * SV_BUF + 64) * 4];
     __shared__ float red[SEQ_T / 64];
     __shared__ float bc;
     SeqScratch &S = *reinterpret_cast<SeqScratch *>(ubuf);
@@ -529,12 +529,16 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     const size_t kv = (size_t)a.n_kv_head * HD;
     const float *vb = a.v_cache + t0 * kv + (size_t)kvh * HD + d0;
     constexpr int R4 = DB / 4;
-    constexpr int NPROD = SEQ_T - 64;  // waves 1.. form the products, wave 0 adds them
+    // wave 0 adds the products; the waves that do not share its SIMD (waves
+    // are dealt to the 4 SIMDs in turn) form them, so the dependent adds
+    // issue back to back
+    constexpr int NPROD = (SEQ_T / 64 - SEQ_T / 256) * 64;
     static_assert(CP * R4 == 2 * NPROD, "two float4 per producer thread per chunk");
     // V loads run PD chunks ahead of the products (a register ring)
     constexpr int PD = 8;
     float4 ring[PD][2];
-    const int pid = tid - 64;
+    const int wv = tid >> 6;
+    const int pid = (wv & 3) ? (wv - (wv >> 2) - 1) * 64 + lane : -1;
     auto issue = [&](float4 (&dst)[2], int c) {
 #pragma unroll
         for (int k = 0; k < 2; k++) {
