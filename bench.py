@@ -13,6 +13,8 @@ Also reported on the same JSON line:
   q4k_matvec     the Q4_K matvec kernel alone at the microbench shapes
                  (configs[1]), GB/s of algorithmic bytes, copies rotated past
                  the 256 MB Infinity Cache
+  matvec_kinds   the same for Q6_K at every shape and the other kinds at
+                 14336x4096
   roofline       the dominant decode kernel (Q4_K matvec, 14336x4096) vs
                  MI355X HBM peak, timed with HIP events on the library stream
   cpu_baseline   the CPU oracle (restated avx2+f16c reference kernels) on a
@@ -217,15 +219,23 @@ def main():
 
     roofline = None
     micro = {}
+    kinds_micro = {}
     if not a.no_micro:
         shapes = [(4096, 4096), (14336, 4096), (4096, 14336), (128256, 4096)]
-        for rows, cols in shapes:
-            ms, copies = time_kernel(aotk, abi.Q4_K, rows, cols)
-            b = matvec_bytes(abi.Q4_K, rows, cols)
+
+        def measure(kind, rows, cols):
+            ms, copies = time_kernel(aotk, kind, rows, cols)
+            b = matvec_bytes(kind, rows, cols)
             gbs = b / (ms * 1e-3) / 1e9
-            micro[f"{rows}x{cols}"] = dict(us=round(ms * 1e3, 2), GBs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4),
-                                          copies=copies)
-            log(f"q4_K matvec {rows}x{cols}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+            log(f"{abi.KIND_NAMES[kind]} matvec {rows}x{cols}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+            return dict(us=round(ms * 1e3, 2), GBs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4), copies=copies)
+
+        for rows, cols in shapes:
+            micro[f"{rows}x{cols}"] = measure(abi.Q4_K, rows, cols)
+        # Q6_K at every shape, the other kinds at the ffn shape
+        kinds_micro["q6_K"] = {f"{r}x{c}": measure(abi.Q6_K, r, c) for r, c in shapes}
+        for kind in (abi.Q5_K, abi.Q8_0, abi.Q4_0, abi.Q5_0, abi.F16, abi.BF16):
+            kinds_micro[abi.KIND_NAMES[kind]] = {"14336x4096": measure(kind, 14336, 4096)}
         dom = micro["14336x4096"]
         roofline = dict(bound="hbm", achieved=dom["GBs"], peak=HBM_PEAK_GBS, unit="GB/s", frac=dom["frac"],
                         traffic=measured_traffic("k_mv_kq<Q4_K> 14336x4096"),
@@ -266,6 +276,7 @@ def main():
         "decode_weight_bytes_per_token": wbytes,
         "decode_weight_GBs": round(wbytes * tok_s / 1e9, 1),
         "q4k_matvec": micro,
+        "matvec_kinds": kinds_micro,
         "other_configs": extra,
         "roofline": roofline,
         "cpu_baseline": cpu,
