@@ -1088,6 +1088,128 @@ __global__ __launch_bounds__(256) void k_mv_float(MvArgs a) {
     }
 }
 
+// F16 / BF16 rows of cols % 64 == 0, cols <= MVH_MAX_COLS: the same eight
+// chains (chain l takes the elements l, l + 8, l + 16, ... of the row, one
+// fmaf each, in order) with wide loads. The 8 lanes of a row load 128
+// contiguous bytes per step (lane l: elements 64t + 8l .. + 7, i.e. one
+// element of every chain) and an 8x8 transpose of 16-bit values over the
+// lanes (three butterfly stages) hands lane l the eight consecutive elements
+// of its own chain. The activation sits in LDS chain-major (xs[l][s] =
+// x[8s + l]), so lane l reads its eight x values as two 16-byte words.
+constexpr int MVH_MAX_COLS = 16128;  // 8 * S floats of LDS stay within 64 KiB
+constexpr int MVH_U = 4;  // 16-byte steps per lane per prefetch batch
+
+__device__ __forceinline__ uint32_t dpp_xor1(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+}
+__device__ __forceinline__ uint32_t dpp_xor2(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+}
+__device__ __forceinline__ uint32_t swz_xor4(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (4 << 10) | 0x1F);  // bit mode: lane ^ 4
+}
+
+// d: halves c = 0..7 of lane l (element (l, c)); afterwards element (c, l).
+__device__ __forceinline__ void transpose8x8_u16(uint32_t d[4], int l) {
+    {  // lane bit 2 <-> position bit 2 (dwords 0,1 <-> 2,3)
+        const bool hi = l & 4;
+        const uint32_t r0 = swz_xor4(hi ? d[0] : d[2]);
+        const uint32_t r1 = swz_xor4(hi ? d[1] : d[3]);
+        if (hi) { d[0] = r0; d[1] = r1; } else { d[2] = r0; d[3] = r1; }
+    }
+    {  // lane bit 1 <-> position bit 1 (dwords 0,2 <-> 1,3)
+        const bool hi = l & 2;
+        const uint32_t r0 = dpp_xor2(hi ? d[0] : d[1]);
+        const uint32_t r1 = dpp_xor2(hi ? d[2] : d[3]);
+        if (hi) { d[0] = r0; d[2] = r1; } else { d[1] = r0; d[3] = r1; }
+    }
+    {  // lane bit 0 <-> position bit 0 (low <-> high halves); byte selectors
+        // by lane parity: send the four halves the partner takes packed in
+        // two dwords, then put the received ones in place
+        const bool hi = l & 1;
+        const uint32_t ssend = hi ? 0x05040100u : 0x07060302u;
+        const uint32_t srcv0 = hi ? 0x07060100u : 0x01000504u;
+        const uint32_t srcv1 = hi ? 0x07060302u : 0x03020504u;
+        const uint32_t r0 = dpp_xor1(__builtin_amdgcn_perm(d[1], d[0], ssend));
+        const uint32_t r1 = dpp_xor1(__builtin_amdgcn_perm(d[3], d[2], ssend));
+        d[0] = __builtin_amdgcn_perm(d[0], r0, srcv0);
+        d[1] = __builtin_amdgcn_perm(d[1], r0, srcv1);
+        d[2] = __builtin_amdgcn_perm(d[2], r1, srcv0);
+        d[3] = __builtin_amdgcn_perm(d[3], r1, srcv1);
+    }
+}
+
+template <int KIND>
+__device__ __forceinline__ float half_lo(uint32_t v) {
+    if (KIND == AOTK_BF16) return __uint_as_float(v << 16);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFF));
+}
+template <int KIND>
+__device__ __forceinline__ float half_hi(uint32_t v) {
+    if (KIND == AOTK_BF16) return __uint_as_float(v & 0xFFFF0000u);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void k_mv_half(MvArgs a) {
+    extern __shared__ float xs[];  // [8][S]
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int tok = blockIdx.y;
+    const int r8 = lane >> 3, l = lane & 7;
+    const int n8 = (int)(a.cols >> 3);
+    const int S = ((n8 + 31) & ~31) + 4;
+    const float *x = a.xf + (size_t)tok * a.cols;
+    for (int i = threadIdx.x; i < (int)a.cols; i += 256) xs[(i & 7) * S + (i >> 3)] = x[i];
+    __syncthreads();
+    const int grow = (blockIdx.x * 4 + wave) * 8 + r8;
+    const bool valid = grow < a.total_rows;
+    int local;
+    const int s = seg_of(a, valid ? grow : 0, local);
+    const uint4 *row = (const uint4 *)(seg_sel(s, a.w[0], a.w[1], a.w[2]) + (size_t)(valid ? local : 0) * a.rb) + l;
+    const float *xl = xs + l * S;
+    const int nt = n8 >> 3;  // 64-element steps
+    float acc = 0.0f;
+    uint4 cur[MVH_U], nxt[MVH_U];
+#pragma unroll
+    for (int u = 0; u < MVH_U; u++) cur[u] = u < nt ? row[8 * u] : make_uint4(0, 0, 0, 0);
+    for (int t0 = 0; t0 < nt; t0 += MVH_U) {
+#pragma unroll
+        for (int u = 0; u < MVH_U; u++) nxt[u] = t0 + MVH_U + u < nt ? row[8 * (t0 + MVH_U + u)] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < MVH_U; u++) {
+            if (t0 + u < nt) {
+                uint32_t d[4] = {cur[u].x, cur[u].y, cur[u].z, cur[u].w};
+                transpose8x8_u16(d, l);
+                const float4 xa = *(const float4 *)(xl + 8 * (t0 + u));
+                const float4 xb = *(const float4 *)(xl + 8 * (t0 + u) + 4);
+                acc = fmaf(half_lo<KIND>(d[0]), xa.x, acc);
+                acc = fmaf(half_hi<KIND>(d[0]), xa.y, acc);
+                acc = fmaf(half_lo<KIND>(d[1]), xa.z, acc);
+                acc = fmaf(half_hi<KIND>(d[1]), xa.w, acc);
+                acc = fmaf(half_lo<KIND>(d[2]), xb.x, acc);
+                acc = fmaf(half_hi<KIND>(d[2]), xb.y, acc);
+                acc = fmaf(half_lo<KIND>(d[3]), xb.z, acc);
+                acc = fmaf(half_hi<KIND>(d[3]), xb.w, acc);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < MVH_U; u++) cur[u] = nxt[u];
+    }
+    // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7))  (simd_avx2.rs:27-34)
+    const float t = acc + shfl_xor(acc, 4);
+    const float u = t + shfl_xor(t, 2);
+    const float v = u + shfl_xor(u, 1);
+    if (l == 0 && valid) store_row(a, grow, tok, v);
+}
+
+static bool mv_half_fits(const MvArgs &a) {
+    if (a.cols % 64 != 0 || a.cols > (size_t)MVH_MAX_COLS) return false;
+    for (int i = 0; i < a.nseg; i++)
+        if ((uintptr_t)a.w[i] % 16 != 0) return false;
+    return true;
+}
+
 // ----------------------------------------------------------------- launch
 
 static MvArgs make_args(int n, const DevWeight *const ws[], float *const ys[], const float *const adds[], const void *x_act) {
@@ -1227,13 +1349,21 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
         }
         break;
     case AOTK_F16:
+    case AOTK_BF16: {
         grid.x = (unsigned)((a.total_rows + 31) / 32);
-        k_mv_float<AOTK_F16><<<grid, 256, 0, s>>>(a);
+        const bool bf = kind == AOTK_BF16;
+        if (mv_half_fits(a) && !getenv("AOTK_NO_MVH")) {
+            const int n8 = (int)(a.cols >> 3);
+            const size_t lds = 8 * sizeof(float) * (size_t)(((n8 + 31) & ~31) + 4);
+            if (bf) k_mv_half<AOTK_BF16><<<grid, 256, lds, s>>>(a);
+            else k_mv_half<AOTK_F16><<<grid, 256, lds, s>>>(a);
+        } else if (bf) {
+            k_mv_float<AOTK_BF16><<<grid, 256, 0, s>>>(a);
+        } else {
+            k_mv_float<AOTK_F16><<<grid, 256, 0, s>>>(a);
+        }
         break;
-    case AOTK_BF16:
-        grid.x = (unsigned)((a.total_rows + 31) / 32);
-        k_mv_float<AOTK_BF16><<<grid, 256, 0, s>>>(a);
-        break;
+    }
     default:
         grid.x = (unsigned)((a.total_rows + 31) / 32);
         k_mv_float<AOTK_F32><<<grid, 256, 0, s>>>(a);

@@ -11,7 +11,7 @@ NAMES = dict(zip(ALL, ["f32", "f16", "bf16", "q4_0", "q5_0", "q8_0", "q4_K", "q5
 
 
 def cols_for(kind):
-    return {F32: [8, 64, 2053, 4096], F16: [8, 64, 2053, 4096], BF16: [12, 64, 2053],
+    return {F32: [8, 64, 2053, 4096], F16: [8, 64, 2053, 4096, 11008, 16384], BF16: [12, 64, 2053, 4096, 14336],
             Q4_0: [32, 96, 2048, 5632], Q5_0: [32, 96, 2048], Q8_0: [32, 96, 2048, 12288],
             Q4_K: [256, 512, 2048, 3072, 5632, 14336, 17408], Q5_K: [256, 512, 2560, 10240],
             Q6_K: [256, 512, 2048, 5632, 14336, 17408]}[kind]
