@@ -1097,31 +1097,34 @@ __global__ __launch_bounds__(256) void k_mv_float(MvArgs a) {
 // of its own chain. The activation sits in LDS chain-major (xs[l][s] =
 // x[8s + l]), so lane l reads its eight x values as two 16-byte words.
 constexpr int MVH_MAX_COLS = 16128;  // 8 * S floats of LDS stay within 64 KiB
-constexpr int MVH_U = 4;  // 16-byte steps per lane per prefetch batch
 
-__device__ __forceinline__ uint32_t dpp_xor1(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+template <int CTRL, int BANKS>
+__device__ __forceinline__ uint32_t dpp_upd(uint32_t old, uint32_t src) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)src, CTRL, 0xF, BANKS, false);
 }
-__device__ __forceinline__ uint32_t dpp_xor2(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-}
-__device__ __forceinline__ uint32_t swz_xor4(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (4 << 10) | 0x1F);  // bit mode: lane ^ 4
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
 }
 
 // d: halves c = 0..7 of lane l (element (l, c)); afterwards element (c, l).
+// Stage m swaps lane bit m with position bit m where they differ.
 __device__ __forceinline__ void transpose8x8_u16(uint32_t d[4], int l) {
-    {  // lane bit 2 <-> position bit 2 (dwords 0,1 <-> 2,3)
-        const bool hi = l & 4;
-        const uint32_t r0 = swz_xor4(hi ? d[0] : d[2]);
-        const uint32_t r1 = swz_xor4(hi ? d[1] : d[3]);
-        if (hi) { d[0] = r0; d[1] = r1; } else { d[2] = r0; d[3] = r1; }
+    {  // bit 2: dwords 2,3 of lanes 0-3 <-> dwords 0,1 of lanes 4-7. row_shr:4
+        // (lane i reads i - 4) written to banks 1,3 (lanes 4-7 of each 8),
+        // row_shl:4 (lane i reads i + 4) to banks 0,2.
+        const uint32_t n0 = dpp_upd<0x114, 0xA>(d[0], d[2]);
+        const uint32_t n1 = dpp_upd<0x114, 0xA>(d[1], d[3]);
+        const uint32_t n2 = dpp_upd<0x104, 0x5>(d[2], d[0]);
+        const uint32_t n3 = dpp_upd<0x104, 0x5>(d[3], d[1]);
+        d[0] = n0; d[1] = n1; d[2] = n2; d[3] = n3;
     }
-    {  // lane bit 1 <-> position bit 1 (dwords 0,2 <-> 1,3)
+    {  // bit 1: dwords 1,3 of lanes {0,1} <-> dwords 0,2 of lanes {2,3} (mod 4);
+        // quad_perm [0,1,0,1] and [2,3,2,3]
         const bool hi = l & 2;
-        const uint32_t r0 = dpp_xor2(hi ? d[0] : d[1]);
-        const uint32_t r1 = dpp_xor2(hi ? d[2] : d[3]);
-        if (hi) { d[0] = r0; d[2] = r1; } else { d[1] = r0; d[3] = r1; }
+        const uint32_t a0 = dpp_mov<0x44>(d[1]), a2 = dpp_mov<0x44>(d[3]);
+        const uint32_t b1 = dpp_mov<0xEE>(d[0]), b3 = dpp_mov<0xEE>(d[2]);
+        if (hi) { d[0] = a0; d[2] = a2; } else { d[1] = b1; d[3] = b3; }
     }
     {  // lane bit 0 <-> position bit 0 (low <-> high halves); byte selectors
         // by lane parity: send the four halves the partner takes packed in
@@ -1130,8 +1133,8 @@ __device__ __forceinline__ void transpose8x8_u16(uint32_t d[4], int l) {
         const uint32_t ssend = hi ? 0x05040100u : 0x07060302u;
         const uint32_t srcv0 = hi ? 0x07060100u : 0x01000504u;
         const uint32_t srcv1 = hi ? 0x07060302u : 0x03020504u;
-        const uint32_t r0 = dpp_xor1(__builtin_amdgcn_perm(d[1], d[0], ssend));
-        const uint32_t r1 = dpp_xor1(__builtin_amdgcn_perm(d[3], d[2], ssend));
+        const uint32_t r0 = dpp_mov<0xB1>(__builtin_amdgcn_perm(d[1], d[0], ssend));  // quad_perm [1,0,3,2]
+        const uint32_t r1 = dpp_mov<0xB1>(__builtin_amdgcn_perm(d[3], d[2], ssend));
         d[0] = __builtin_amdgcn_perm(d[0], r0, srcv0);
         d[1] = __builtin_amdgcn_perm(d[1], r0, srcv1);
         d[2] = __builtin_amdgcn_perm(d[2], r1, srcv0);
@@ -1150,7 +1153,7 @@ __device__ __forceinline__ float half_hi(uint32_t v) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
 }
 
-template <int KIND>
+template <int KIND, int MVH_U>
 __global__ __launch_bounds__(256) void k_mv_half(MvArgs a) {
     extern __shared__ float xs[];  // [8][S]
     const int lane = threadIdx.x & 63;
@@ -1159,43 +1162,67 @@ __global__ __launch_bounds__(256) void k_mv_half(MvArgs a) {
     const int r8 = lane >> 3, l = lane & 7;
     const int n8 = (int)(a.cols >> 3);
     const int S = ((n8 + 31) & ~31) + 4;
-    const float *x = a.xf + (size_t)tok * a.cols;
-    for (int i = threadIdx.x; i < (int)a.cols; i += 256) xs[(i & 7) * S + (i >> 3)] = x[i];
-    __syncthreads();
     const int grow = (blockIdx.x * 4 + wave) * 8 + r8;
     const bool valid = grow < a.total_rows;
     int local;
     const int s = seg_of(a, valid ? grow : 0, local);
     const uint4 *row = (const uint4 *)(seg_sel(s, a.w[0], a.w[1], a.w[2]) + (size_t)(valid ? local : 0) * a.rb) + l;
-    const float *xl = xs + l * S;
-    const int nt = n8 >> 3;  // 64-element steps
-    float acc = 0.0f;
+    const int nt = n8 >> 3;  // 64-element steps (>= 1)
+    // The activation goes to LDS chain-major; its first 4096 elements are
+    // loaded before the first weights (the wait for them then leaves the
+    // weight loads in flight).
+    const float4 *x4 = (const float4 *)(a.xf + (size_t)tok * a.cols);
+    const int n4 = (int)(a.cols >> 2);
+    auto put_x = [&](int i4, const float4 &v) {  // elements 4 i4 .. + 3: chains (4 i4) & 7 .. + 3
+        const int i = 4 * i4;
+        float *p = xs + (i & 7) * S + (i >> 3);
+        p[0] = v.x;
+        p[S] = v.y;
+        p[2 * S] = v.z;
+        p[3 * S] = v.w;
+    };
+    float4 xv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) xv[k] = x4[min((int)threadIdx.x + 256 * k, n4 - 1)];
+    // Loads past the row's end re-read its last step (always in bounds, so
+    // every load is unconditional and the waits stay exact).
+    auto ld = [&](int t) { return row[8 * min(t, nt - 1)]; };
     uint4 cur[MVH_U], nxt[MVH_U];
 #pragma unroll
-    for (int u = 0; u < MVH_U; u++) cur[u] = u < nt ? row[8 * u] : make_uint4(0, 0, 0, 0);
-    for (int t0 = 0; t0 < nt; t0 += MVH_U) {
+    for (int u = 0; u < MVH_U; u++) cur[u] = ld(u);
 #pragma unroll
-        for (int u = 0; u < MVH_U; u++) nxt[u] = t0 + MVH_U + u < nt ? row[8 * (t0 + MVH_U + u)] : make_uint4(0, 0, 0, 0);
+    for (int k = 0; k < 4; k++)
+        if ((int)threadIdx.x + 256 * k < n4) put_x(threadIdx.x + 256 * k, xv[k]);
+    for (int i4 = threadIdx.x + 1024; i4 < n4; i4 += 256) put_x(i4, x4[i4]);
+    __syncthreads();
+    const float *xl = xs + l * S;
+    float acc = 0.0f;
+    auto step = [&](const uint4 &w, int t) {
+        uint32_t d[4] = {w.x, w.y, w.z, w.w};
+        transpose8x8_u16(d, l);
+        const float4 xa = *(const float4 *)(xl + 8 * t);
+        const float4 xb = *(const float4 *)(xl + 8 * t + 4);
+        acc = fmaf(half_lo<KIND>(d[0]), xa.x, acc);
+        acc = fmaf(half_hi<KIND>(d[0]), xa.y, acc);
+        acc = fmaf(half_lo<KIND>(d[1]), xa.z, acc);
+        acc = fmaf(half_hi<KIND>(d[1]), xa.w, acc);
+        acc = fmaf(half_lo<KIND>(d[2]), xb.x, acc);
+        acc = fmaf(half_hi<KIND>(d[2]), xb.y, acc);
+        acc = fmaf(half_lo<KIND>(d[3]), xb.z, acc);
+        acc = fmaf(half_hi<KIND>(d[3]), xb.w, acc);
+    };
+    int t0 = 0;
+    for (; t0 + MVH_U <= nt; t0 += MVH_U) {
 #pragma unroll
-        for (int u = 0; u < MVH_U; u++) {
-            if (t0 + u < nt) {
-                uint32_t d[4] = {cur[u].x, cur[u].y, cur[u].z, cur[u].w};
-                transpose8x8_u16(d, l);
-                const float4 xa = *(const float4 *)(xl + 8 * (t0 + u));
-                const float4 xb = *(const float4 *)(xl + 8 * (t0 + u) + 4);
-                acc = fmaf(half_lo<KIND>(d[0]), xa.x, acc);
-                acc = fmaf(half_hi<KIND>(d[0]), xa.y, acc);
-                acc = fmaf(half_lo<KIND>(d[1]), xa.z, acc);
-                acc = fmaf(half_hi<KIND>(d[1]), xa.w, acc);
-                acc = fmaf(half_lo<KIND>(d[2]), xb.x, acc);
-                acc = fmaf(half_hi<KIND>(d[2]), xb.y, acc);
-                acc = fmaf(half_lo<KIND>(d[3]), xb.z, acc);
-                acc = fmaf(half_hi<KIND>(d[3]), xb.w, acc);
-            }
-        }
+        for (int u = 0; u < MVH_U; u++) nxt[u] = ld(t0 + MVH_U + u);
+#pragma unroll
+        for (int u = 0; u < MVH_U; u++) step(cur[u], t0 + u);
 #pragma unroll
         for (int u = 0; u < MVH_U; u++) cur[u] = nxt[u];
     }
+#pragma unroll
+    for (int u = 0; u < MVH_U; u++)
+        if (t0 + u < nt) step(cur[u], t0 + u);
     // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7))  (simd_avx2.rs:27-34)
     const float t = acc + shfl_xor(acc, 4);
     const float u = t + shfl_xor(t, 2);
@@ -1355,8 +1382,14 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
         if (mv_half_fits(a) && !getenv("AOTK_NO_MVH")) {
             const int n8 = (int)(a.cols >> 3);
             const size_t lds = 8 * sizeof(float) * (size_t)(((n8 + 31) & ~31) + 4);
-            if (bf) k_mv_half<AOTK_BF16><<<grid, 256, lds, s>>>(a);
-            else k_mv_half<AOTK_F16><<<grid, 256, lds, s>>>(a);
+            // deeper prefetch when few rows leave few waves in flight
+            if (a.total_rows < 16384) {
+                if (bf) k_mv_half<AOTK_BF16, 8><<<grid, 256, lds, s>>>(a);
+                else k_mv_half<AOTK_F16, 8><<<grid, 256, lds, s>>>(a);
+            } else {
+                if (bf) k_mv_half<AOTK_BF16, 4><<<grid, 256, lds, s>>>(a);
+                else k_mv_half<AOTK_F16, 4><<<grid, 256, lds, s>>>(a);
+            }
         } else if (bf) {
             k_mv_float<AOTK_BF16><<<grid, 256, 0, s>>>(a);
         } else {

@@ -76,6 +76,20 @@ def test_matvec_bitexact(aotk, oracle, kind):
         assert np.array_equal(got2.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("kind", [F16, BF16], ids=lambda k: NAMES[k])
+def test_matvec_half_many_rows(aotk, oracle, kind):
+    """The shallow-prefetch variant for matrices of 16384 rows or more, and a
+    ragged last block of rows."""
+    rng = np.random.default_rng(31)
+    rows, cols = 16421, 192
+    raw = weights(kind, rows, cols, 5, oracle)
+    x = (rng.standard_normal(cols) * 2).astype(np.float32)
+    act = oracle.quantize_act(kind, x)
+    ref = oracle.matvec(kind, raw, act, rows, cols)
+    got = aotk.matvec(aotk.Weight(kind, raw, rows, cols), act)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("kind", [Q4_K, Q6_K, Q8_0, Q5_K, F16], ids=lambda k: NAMES[k])
 def test_matmul_equals_matvec(aotk, oracle, kind):
     rng = np.random.default_rng(7)
