@@ -18,18 +18,6 @@ template <int CTRL>
 __device__ __forceinline__ float dppx_f(float v) { return __int_as_float(dppx_i<CTRL>(__float_as_int(v))); }
 constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
 
-// (|value|, index) reduction keeping the largest value, the smallest index
-// among equals (the first index of the maximum).
-template <int CTRL>
-__device__ __forceinline__ void amax_step(float &amax, int &idx) {
-    const float oa = dppx_f<CTRL>(amax);
-    const int oi = dppx_i<CTRL>(idx);
-    if (oa > amax || (oa == amax && oi < idx)) {
-        amax = oa;
-        idx = oi;
-    }
-}
-
 // One lane's share of a Q8_K block (quant.rs:248-283) of 256 values held 4
 // per lane (element 4*lane + k) of a wave: the 4 packed quants, the sum of
 // the lane's quad of 4 lanes (lanes 4j hold bsums[j]) and the block scale d.
@@ -38,45 +26,47 @@ struct Q8KLane {
     int quad_sum;
     float d;
 };
+// |f| as an integer of the same order; NaN maps to 0, below every value,
+// as the reference's strict '>' scan from 0 never picks a NaN.
+__device__ __forceinline__ uint32_t mag_bits(float f) {
+    const uint32_t b = __float_as_uint(f) & 0x7FFFFFFFu;
+    return b > 0x7F800000u ? 0u : b;
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dppx_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+
 __device__ __forceinline__ Q8KLane q8k_lane(const float v[4], int lane) {
-    float amax = 0.0f;
-    int idx = 0x7fffffff;
-    for (int k = 0; k < 4; k++) {
-        float a = fabsf(v[k]);
-        if (a > amax) { amax = a; idx = lane * 4 + k; }
-    }
-    amax_step<DPP_XOR1>(amax, idx);
-    amax_step<DPP_XOR2>(amax, idx);
-    amax_step<DPP_HALF_MIRROR>(amax, idx);
-    amax_step<DPP_MIRROR>(amax, idx);
-    // the four rows of 16 lanes, in index order
-    {
-        float ra = readlane_f(amax, 0);
-        int ri = __builtin_amdgcn_readlane(idx, 0);
+    // the largest magnitude over the wave, as ordered integers
+    uint32_t m[4];
 #pragma unroll
-        for (int r = 1; r < 4; r++) {
-            const float oa = readlane_f(amax, 16 * r);
-            const int oi = __builtin_amdgcn_readlane(idx, 16 * r);
-            if (oa > ra || (oa == ra && oi < ri)) {
-                ra = oa;
-                ri = oi;
-            }
-        }
-        amax = ra;
-        idx = ri;
-    }
-    const int src_lane = (idx == 0x7fffffff) ? 0 : idx >> 2, sk = idx & 3;
-    const float c0 = readlane_f(v[0], src_lane), c1 = readlane_f(v[1], src_lane);
-    const float c2 = readlane_f(v[2], src_lane), c3 = readlane_f(v[3], src_lane);
-    float max = sk == 0 ? c0 : (sk == 1 ? c1 : (sk == 2 ? c2 : c3));
+    for (int k = 0; k < 4; k++) m[k] = mag_bits(v[k]);
+    uint32_t a = max(max(m[0], m[1]), max(m[2], m[3]));
+    a = max(a, dppx_u<DPP_XOR1>(a));
+    a = max(a, dppx_u<DPP_XOR2>(a));
+    a = max(a, dppx_u<DPP_HALF_MIRROR>(a));
+    a = max(a, dppx_u<DPP_MIRROR>(a));
+    const uint32_t amax = max(max((uint32_t)__builtin_amdgcn_readlane((int)a, 0), (uint32_t)__builtin_amdgcn_readlane((int)a, 16)),
+                              max((uint32_t)__builtin_amdgcn_readlane((int)a, 32), (uint32_t)__builtin_amdgcn_readlane((int)a, 48)));
+    // its first index 4 * lane + k: the lowest lane holding it, then that
+    // lane's lowest k
+    const int kl = m[0] == amax ? 0 : (m[1] == amax ? 1 : (m[2] == amax ? 2 : (m[3] == amax ? 3 : 4)));
+    const unsigned long long hit = __ballot(kl < 4);
+    const int src_lane = hit ? (int)__builtin_ctzll(hit) : 0;
+    const int sk = __builtin_amdgcn_readlane(kl, src_lane);
+    const float pick = sk == 0 ? v[0] : (sk == 1 ? v[1] : (sk == 2 ? v[2] : v[3]));
+    const float max = readlane_f(pick, src_lane);
     Q8KLane r;
     r.packed = 0;
     int sum = 0;
     r.d = 0.0f;
-    if (amax != 0.0f) {
-        float iscale = -127.0f / max;
+    if (amax != 0u) {  // all zeros (or all NaN: the scan never moves off 0) give a zero block
+        const float iscale = -127.0f / max;
+#pragma unroll
         for (int k = 0; k < 4; k++) {
-            int t = round_i(iscale * v[k]);
+            // Rust's saturating `as i32` (NaN -> 0) is the conversion's own behaviour
+            int t = (int)roundf(iscale * v[k]);
             t = t > 127 ? 127 : t;
             r.packed |= (uint32_t)(t & 0xFF) << (8 * k);
             sum += (int8_t)t;

@@ -153,6 +153,10 @@ struct SampleArgs {
 };
 size_t sampler_scratch_bytes(size_t vocab);
 void launch_sample(const SampleArgs &p, hipStream_t s);
+// One token through a K-quant matrix of <= 64 super-blocks per row, the f32
+// input quantized to Q8_K inside the launch (same bytes as launch_quant_f32).
+// Returns false (nothing launched) for other kinds and widths.
+bool launch_matvec_quant(const DevWeight &w, const float *x, float *y, const float *add, hipStream_t s);
 void launch_matvec_multi(int n, const DevWeight *const ws[], float *const ys[], const void *x_act, size_t m,
                          hipStream_t s);
 // Matrices of a Q4_K/Q5_K kind (up to three, e.g. q and k) and one Q6_K

@@ -12,6 +12,7 @@
 //     sum, then the scalar tail.
 // Weights are streamed once with 16-byte loads; the input vector is tiny and
 // stays in L2/L1.
+#include "actfn.hpp"
 #include "device.hpp"
 #include "internal.hpp"
 
@@ -40,6 +41,9 @@ struct MvArgs {
     const float *xd;
     const int16_t *xbs;
     const float *xf;
+    // K-quant rows, one token: when set, every block quantizes this f32
+    // input to Q8_K itself (instead of reading xq / xd / xbs)
+    const float *xq_src;
 };
 
 // Segment of a global row (constant indices only, so that the kernel
@@ -389,7 +393,31 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
     MV_TS(0);
     load(cur, dcur, 0);  // weights first: the longest latency
     // stage this token's Q8_K activation in LDS
-    {
+    if (a.xq_src) {
+        // quantize the f32 input here, wave w taking super-blocks w, w + 4,
+        // ... (the device quantizer of k_quant_f32, quant.rs:248-283)
+        for (int b0 = wave; b0 < nb; b0 += 16) {
+            float4 v4[4];  // four super-blocks' loads in flight together
+#pragma unroll
+            for (int k = 0; k < 4; k++) v4[k] = ((const float4 *)(a.xq_src + (size_t)min(b0 + 4 * k, nb - 1) * 256))[lane];
+            Q8KLane rq[4];  // independent: their reductions interleave
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float v[4] = {v4[k].x, v4[k].y, v4[k].z, v4[k].w};
+                rq[k] = q8k_lane(v, lane);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int b = b0 + 4 * k;
+                if (b >= nb) break;
+                const Q8KLane &r = rq[k];
+                uint8_t *recb = sY + b * KQ_REC;
+                ((uint32_t *)recb)[lane] = r.packed;
+                if ((lane & 3) == 0) ((int16_t *)(recb + 256))[lane >> 2] = (int16_t)r.quad_sum;
+                if (lane == 0) *(float *)(recb + 288) = r.d;
+            }
+        }
+    } else {
         const uint4 *xq = (const uint4 *)(a.xq + (size_t)tok * a.cols);
         for (int i = tid; i < nb * 16; i += 256) *(uint4 *)(sY + (i >> 4) * KQ_REC + (i & 15) * 16) = xq[i];
         const uint4 *xb = (const uint4 *)(a.xbs + (size_t)tok * nb * 16);
@@ -1416,6 +1444,23 @@ void launch_matvec_multi(int n, const DevWeight *const ws[], float *const ys[], 
                          hipStream_t s) {
     MvArgs a = make_args(n, ws, ys, nullptr, x_act);
     launch_args(ws[0]->kind, a, m, s);
+}
+
+bool launch_matvec_quant(const DevWeight &w, const float *x, float *y, const float *add, hipStream_t s) {
+    const int kind = w.kind;
+    if ((kind != AOTK_Q4_K && kind != AOTK_Q5_K && kind != AOTK_Q6_K) || w.nb > 64 || getenv("AOTK_NO_MVQ"))
+        return false;
+    const DevWeight *ws[1] = {&w};
+    float *ys[1] = {y};
+    const float *adds[1] = {add};
+    ActQ8K none = {};
+    MvArgs a = make_args(1, ws, ys, adds, &none);
+    a.xq_src = x;
+    dim3 grid(1, 1);
+    if (kind == AOTK_Q4_K) launch_kq<AOTK_Q4_K>(a, grid, s);
+    else if (kind == AOTK_Q5_K) launch_kq<AOTK_Q5_K>(a, grid, s);
+    else launch_kq<AOTK_Q6_K>(a, grid, s);
+    return true;
 }
 
 bool matvec_pair_ok(const DevWeight &a, const DevWeight &b) {

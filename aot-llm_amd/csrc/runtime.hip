@@ -958,13 +958,14 @@ static void run_layers(aotk_state *st, size_t m, size_t pos0, const int *pos_dev
             launch_attention(st->xb, st->q, kc, vc, d.n_head, d.n_kv_head, d.head_dim, st->ctx, pos0, m, window,
                              pos_dev, st->attn_ws, st->attn_ws_bytes, s);
         }
-        if (activation(L.wo.kind) != ACT_F32) launch_quant_f32(st->xb, qd, m, outs_for(st, {L.wo.kind}, nullptr), s);
-        if (f.post_norms) {
-            launch_matvec(L.wo, act_for(st, L.wo.kind, st->xb), m, st->xb2, nullptr, s);
-            launch_rmsnorm_add(st->x, st->xb2, L.attn_post_norm, dim, m, d.eps, s);
-        } else {
-            launch_matvec(L.wo, act_for(st, L.wo.kind, st->xb), m, st->x, st->x, s);
+        // decode: the attention output is quantized inside the wo launch where the kind allows
+        float *wo_y = f.post_norms ? st->xb2 : st->x;
+        const float *wo_add = f.post_norms ? nullptr : st->x;
+        if (!(m == 1 && launch_matvec_quant(L.wo, st->xb, wo_y, wo_add, s))) {
+            if (activation(L.wo.kind) != ACT_F32) launch_quant_f32(st->xb, qd, m, outs_for(st, {L.wo.kind}, nullptr), s);
+            launch_matvec(L.wo, act_for(st, L.wo.kind, st->xb), m, wo_y, wo_add, s);
         }
+        if (f.post_norms) launch_rmsnorm_add(st->x, st->xb2, L.attn_post_norm, dim, m, d.eps, s);
         // feed-forward block
         launch_rmsnorm_quant(st->x, L.ffn_norm, dim, m, d.eps, outs_for(st, {L.gate.kind, L.up.kind}, st->xb), s);
         bool same2 = L.gate.kind == L.up.kind && activation(L.gate.kind) != ACT_F32;
