@@ -121,10 +121,17 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant(const float *__restrict
         const int i = threadIdx.x + k * SEQ_T;
         wv[k] = i < n ? w[i] : 0.0f;
     }
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float v = xr[i];
-        row[i] = v;
-        sq[seq_idx(i, C)] = v * v;
+    // all of a thread's loads are in flight together (n <= 8 * blockDim.x)
+    float xv[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) xv[k] = xr[min((int)threadIdx.x + k * SEQ_T, n - 1)];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i = threadIdx.x + k * SEQ_T;
+        if (i < n) {
+            row[i] = xv[k];
+            sq[seq_idx(i, C)] = xv[k] * xv[k];
+        }
     }
     __syncthreads();
     RMS_TS(1);
@@ -831,24 +838,36 @@ void launch_add(float *x, const float *y, size_t n, hipStream_t s) {
 
 // Gemma post-norm join: x += rmsnorm(y) (emit.rs:320-324).
 __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_add(float *x, const float *y, const float *w, int n, float eps) {
-    __shared__ __align__(16) float row[8192];
     __shared__ float sq[SEQ_PAD_N];
     __shared__ SeqScratch S;
     const size_t m = blockIdx.x;
     const float *yr = y + m * n;
     float *xr = x + m * n;
     const int C = seq_chunk(n);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float v = yr[i];
-        row[i] = v;
-        sq[seq_idx(i, C)] = v * v;
+    // every load (y, and x and w for the update) is issued before the sum
+    float yv[8], xv[8], wv[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i = min((int)threadIdx.x + k * SEQ_T, n - 1);
+        yv[k] = yr[i];
+        xv[k] = xr[i];
+        wv[k] = w[i];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i = threadIdx.x + k * SEQ_T;
+        if (i < n) sq[seq_idx(i, C)] = yv[k] * yv[k];
     }
     __syncthreads();
     RMS_TS(1);
     float ss = exact_seq_sum(sq, n, S);
     RMS_TS(2);
     float r = 1.0f / sqrtf(ss / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) xr[i] = xr[i] + row[i] * r * w[i];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i = threadIdx.x + k * SEQ_T;
+        if (i < n) xr[i] = xv[k] + yv[k] * r * wv[k];
+    }
 }
 void launch_rmsnorm_add(float *x, const float *y, const float *w, size_t n, size_t m, float eps, hipStream_t s) {
     k_rmsnorm_add<<<(unsigned)m, SEQ_T, 0, s>>>(x, y, w, (int)n, eps);
