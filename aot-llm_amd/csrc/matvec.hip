@@ -279,28 +279,62 @@ struct KqGeom {
 // super-block's record with 16-byte loads hit disjoint banks.
 constexpr int KQ_REC = 304;
 
-template <int KIND>
-__device__ __forceinline__ float kq_term(const uint4 (&c)[KqGeom<KIND>::CH], float d6, const uint8_t *rec) {
+// Rows of <= 32 super-blocks split each super-block over two lanes (SPL = 2):
+// lane h of the pair takes the first or the second half of the 256 values
+// (Q4_K/Q5_K sub-blocks 4h..4h+3, Q6_K 16-value groups 8h..8h+7), the pair
+// adds its integer sums (exact, so the split changes nothing) and both form
+// the f32 term. The chunks a lane holds, in the order kq_sums reads them:
+//   Q4_K: header, then the 4 qs chunks of its half;
+//   Q5_K: header, the 2 qh chunks, the 4 qs chunks of its half;
+//   Q6_K: the 4 ql chunks and 2 qh chunks of its half, the scales.
+template <int KIND, int SPL>
+__device__ __forceinline__ constexpr int kq_chl() {
+    return SPL == 1 ? KqGeom<KIND>::CH : (KIND == AOTK_Q4_K ? 5 : 7);
+}
+template <int KIND, int SPL>
+__device__ __forceinline__ int kq_chunk(int k, int h) {
+    if (SPL == 1) return k;
+    if (KIND == AOTK_Q4_K) return k == 0 ? 0 : 1 + 4 * h + (k - 1);
+    if (KIND == AOTK_Q5_K) return k < 3 ? k : 3 + 4 * h + (k - 3);
+    return k < 4 ? 4 * h + k : (k < 6 ? 8 + 2 * h + (k - 4) : 12);
+}
+
+// The exact integer sums of one lane's share of a super-block (sumi: the
+// scaled dot products; summ: the mins against the bsums) and, after the
+// pair's exchange, the f32 term d*sumi - dmin*summ of quant.rs/matvec.rs.
+template <int KIND, int SPL>
+__device__ __forceinline__ float kq_term(const uint4 (&c)[kq_chl<KIND, SPL>()], float d6, const uint8_t *rec, int h) {
     const float yd = *(const float *)(rec + 288);
-    const uint4 b0 = *(const uint4 *)(rec + 256), b1 = *(const uint4 *)(rec + 272);
-    const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-    auto bs = [&](int g) { return (int)(int16_t)((bw[g >> 1] >> (16 * (g & 1))) & 0xFFFFu); };
+    const uint8_t *rh = rec + 128 * h;  // this lane's half of the activation
+    constexpr int NBW = 8 / SPL;         // bsum words of the lane's share
+    uint32_t bw[NBW];
+#pragma unroll
+    for (int q = 0; q < NBW / 4; q++) {
+        const uint4 b = *(const uint4 *)(rec + 256 + 16 * (h * (NBW / 4) + q));
+        bw[4 * q] = b.x;
+        bw[4 * q + 1] = b.y;
+        bw[4 * q + 2] = b.z;
+        bw[4 * q + 3] = b.w;
+    }
+    auto bs = [&](int g) { return (int)(int16_t)((bw[g >> 1] >> (16 * (g & 1))) & 0xFFFFu); };  // local group
     int sumi = 0;
     if (KIND == AOTK_Q4_K || KIND == AOTK_Q5_K) {
         constexpr int QC = KIND == AOTK_Q4_K ? 1 : 3;
+        constexpr int NJ = 4 / SPL;  // 64-value sub-block pairs of the lane
         const uint4 hdr = c[0];
         int summ = 0;
         uint32_t hq[8];
         if (KIND == AOTK_Q5_K) {
-            hq[0] = c[1].x; hq[1] = c[1].y; hq[2] = c[1].z; hq[3] = c[1].w;
-            hq[4] = c[2].x; hq[5] = c[2].y; hq[6] = c[2].z; hq[7] = c[2].w;
+            const int sh = 2 * NJ * h;  // the qh bits of the lane's first pair
+            hq[0] = c[1].x >> sh; hq[1] = c[1].y >> sh; hq[2] = c[1].z >> sh; hq[3] = c[1].w >> sh;
+            hq[4] = c[2].x >> sh; hq[5] = c[2].y >> sh; hq[6] = c[2].z >> sh; hq[7] = c[2].w >> sh;
         }
 #pragma unroll
-        for (int jp = 0; jp < 4; jp++) {
-            const uint4 q0 = c[QC + 2 * jp], q1 = c[QC + 2 * jp + 1];
+        for (int j = 0; j < NJ; j++) {
+            const uint4 q0 = c[QC + 2 * j], q1 = c[QC + 2 * j + 1];
             const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-            const uint4 l0 = *(const uint4 *)(rec + 64 * jp), l1 = *(const uint4 *)(rec + 64 * jp + 16);
-            const uint4 h0 = *(const uint4 *)(rec + 64 * jp + 32), h1 = *(const uint4 *)(rec + 64 * jp + 48);
+            const uint4 l0 = *(const uint4 *)(rh + 64 * j), l1 = *(const uint4 *)(rh + 64 * j + 16);
+            const uint4 h0 = *(const uint4 *)(rh + 64 * j + 32), h1 = *(const uint4 *)(rh + 64 * j + 48);
             const uint32_t yl[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
             const uint32_t yh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
             int slo = 0, shi = 0;
@@ -309,32 +343,55 @@ __device__ __forceinline__ float kq_term(const uint4 (&c)[KqGeom<KIND>::CH], flo
                 uint32_t lo = qw[k] & 0x0F0F0F0Fu;
                 uint32_t hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
                 if (KIND == AOTK_Q5_K) {
-                    lo |= ((hq[k] >> (2 * jp)) & 0x01010101u) << 4;
-                    hi |= ((hq[k] >> (2 * jp + 1)) & 0x01010101u) << 4;
+                    lo |= ((hq[k] >> (2 * j)) & 0x01010101u) << 4;
+                    hi |= ((hq[k] >> (2 * j + 1)) & 0x01010101u) << 4;
                 }
                 slo = dot4(lo, yl[k], slo);
                 shi = dot4(hi, yh[k], shi);
             }
             int sc0, m0, sc1, m1;
-            scale_min_k4(2 * jp, hdr.y, hdr.z, hdr.w, sc0, m0);
-            scale_min_k4(2 * jp + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
+            if (SPL == 1) {
+                scale_min_k4(2 * j, hdr.y, hdr.z, hdr.w, sc0, m0);
+                scale_min_k4(2 * j + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
+            } else {  // sub-blocks 2j, 2j + 1 of the lane's half: 4h + 2j, 4h + 2j + 1
+                int a0, b0, a1, b1, c0, e0, c1, e1;
+                scale_min_k4(2 * j, hdr.y, hdr.z, hdr.w, a0, b0);
+                scale_min_k4(2 * j + 1, hdr.y, hdr.z, hdr.w, a1, b1);
+                scale_min_k4(4 + 2 * j, hdr.y, hdr.z, hdr.w, c0, e0);
+                scale_min_k4(4 + 2 * j + 1, hdr.y, hdr.z, hdr.w, c1, e1);
+                sc0 = h ? c0 : a0;
+                m0 = h ? e0 : b0;
+                sc1 = h ? c1 : a1;
+                m1 = h ? e1 : b1;
+            }
             // 24-bit multiplies (full rate): every factor fits in 24 bits
             sumi += __mul24(sc0, slo) + __mul24(sc1, shi);
-            summ += __mul24(m0, bs(4 * jp) + bs(4 * jp + 1)) + __mul24(m1, bs(4 * jp + 2) + bs(4 * jp + 3));
+            summ += __mul24(m0, bs(4 * j) + bs(4 * j + 1)) + __mul24(m1, bs(4 * j + 2) + bs(4 * j + 3));
             asm volatile("" ::: "memory");  // keep the activation reads local
+        }
+        if (SPL == 2) {
+            sumi += dppx_i<DPP_XOR1>(sumi);
+            summ += dppx_i<DPP_XOR1>(summ);
         }
         const float dd = f16_to_f32(hdr.x & 0xFFFFu) * yd;
         const float dm = f16_to_f32(hdr.x >> 16) * yd;
         return dd * (float)sumi - dm * (float)summ;
     } else {
-        const uint4 scv = c[12];
-        const uint32_t scw[4] = {scv.x, scv.y, scv.z, scv.w};
+        constexpr int NG = 16 / SPL;  // 16-value groups of the lane
+        const uint4 scv = c[kq_chl<KIND, SPL>() - 1];
+        uint32_t scw[NG / 4];
+        if (SPL == 1) {
+            scw[0] = scv.x; scw[1] = scv.y; scw[NG / 4 - 2] = scv.z; scw[NG / 4 - 1] = scv.w;
+        } else {
+            scw[0] = h ? scv.z : scv.x;
+            scw[1] = h ? scv.w : scv.y;
+        }
 #pragma unroll
-        for (int g = 0; g < 16; g++) {
+        for (int g = 0; g < NG; g++) {
             const int n = g >> 3, quarter = (g & 7) >> 1, half = g & 1;
-            const uint4 l4 = c[4 * n + 2 * (quarter & 1) + half];
-            const uint4 h4 = c[8 + 2 * n + half];
-            const uint4 y4 = *(const uint4 *)(rec + 16 * g);
+            const uint4 l4 = SPL == 1 ? c[4 * n + 2 * (quarter & 1) + half] : c[2 * (quarter & 1) + half];
+            const uint4 h4 = SPL == 1 ? c[8 + 2 * n + half] : c[4 + half];
+            const uint4 y4 = *(const uint4 *)(rh + 16 * g);
             const uint32_t lw[4] = {l4.x, l4.y, l4.z, l4.w};
             const uint32_t hw[4] = {h4.x, h4.y, h4.z, h4.w};
             const uint32_t yw[4] = {y4.x, y4.y, y4.z, y4.w};
@@ -349,10 +406,15 @@ __device__ __forceinline__ float kq_term(const uint4 (&c)[KqGeom<KIND>::CH], flo
             sumi += __mul24(sc, sg - 32 * bs(g));  // |sg - 32 bs| < 2^18
             if ((g & 3) == 3) asm volatile("" ::: "memory");  // keep the activation reads local
         }
+        if (SPL == 2) sumi += dppx_i<DPP_XOR1>(sumi);
         const float dd = d6 * yd;
         return dd * (float)sumi;
     }
 }
+
+// Lanes per super-block: two for the row widths with their own
+// instantiation up to 32 super-blocks, else one.
+__host__ __device__ constexpr int kq_spl(int nb) { return nb > 0 && nb <= 32 ? 2 : 1; }
 
 // PF = 0: one row group per wave (G == 1), register budget for 4 waves per
 // SIMD; PF = 1: G groups per wave with the next group's loads in flight.
@@ -362,12 +424,15 @@ __device__ __forceinline__ float kq_term(const uint4 (&c)[KqGeom<KIND>::CH], flo
 template <int KIND, int PF, int NB>
 __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int bx, uint8_t *sY, float (*sT)[256 + 16]) {
     using Geo = KqGeom<KIND>;
-    constexpr int CH = Geo::CH;
+    constexpr int SPL = kq_spl(NB);
+    constexpr int CH = kq_chl<KIND, SPL>();
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tok = blockIdx.y;
     const int nb = NB > 0 ? NB : a.nb;
-    if (NB > 0) RL = 64 / NB;
-    const int rs = lane / nb, s = lane - rs * nb;
+    if (NB > 0) RL = 64 / (SPL * NB);
+    const int h = SPL == 2 ? lane & 1 : 0;  // half of the super-block
+    const int li = SPL == 2 ? lane >> 1 : lane;
+    const int rs = li / nb, s = li - rs * nb;
     const bool lane_on = rs < RL;
     const int sa = lane_on ? s : 0;
     const size_t cs = (size_t)nb * 16;
@@ -386,7 +451,7 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
         const int sg = seg_of(a, on ? row : 0, local);
         const uint8_t *wp = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * rowb + (size_t)sa * 16;
 #pragma unroll
-        for (int k = 0; k < CH; k++) c[k] = *(const uint4 *)(wp + k * cs);
+        for (int k = 0; k < CH; k++) c[k] = *(const uint4 *)(wp + kq_chunk<KIND, SPL>(k, h) * cs);
         if (KIND == AOTK_Q6_K)
             d6 = f16_to_f32(((const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]))[(size_t)local * nb + sa]);
     };
@@ -432,9 +497,9 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
     // at a time ahead of the dependent adds), the store
     auto group = [&](const uint4 *c, float d6, int gi) {
         const int gr0 = (group0 + gi) * RL;
-        const float term = kq_term<KIND>(*(const uint4(*)[CH])c, d6, rec);
+        const float term = kq_term<KIND, SPL>(*(const uint4(*)[CH])c, d6, rec, h);
         MV_TS(2 + 2 * gi);
-        if (lane_on) sT[wave][rs * ts + s] = term;
+        if (lane_on && h == 0) sT[wave][rs * ts + s] = term;
         wave_lds_sync();
         if (lane < RL && gr0 + lane < a.total_rows) {
             const float4 *tp = (const float4 *)&sT[wave][lane * ts];
@@ -1303,10 +1368,18 @@ static MvArgs make_args(int n, const DevWeight *const ws[], float *const ys[], c
 // Row slots per wave (RL), row groups per wave (G) and blocks of the
 // K-quant kernel: all waves resident in one round (3 waves per SIMD on 256
 // CUs), each doing G row groups.
+static bool nb_specialized(int nb) {
+    return nb == 8 || nb == 10 || nb == 16 || nb == 22 || nb == 40 || nb == 48 || nb == 56;
+}
+
 static void kq_shape(const MvArgs &a, int &RL, int &G, int &blocks) {
-    RL = 64 / a.nb;  // rows per group: every lane slot of nb lanes that fits
+    // rows per group: every lane slot of spl * nb lanes that fits
+    RL = 64 / (kq_spl(nb_specialized(a.nb) ? a.nb : 0) * a.nb);
     const int groups = (a.total_rows + RL - 1) / RL;
-    G = (groups + 3071) / 3072;
+    // groups per wave: one while the launch has at most 3072 groups of the
+    // unsplit size (groups of the two-lane split hold half as many rows)
+    const int gcap = 3072 * (64 / a.nb) / RL;
+    G = (groups + gcap - 1) / gcap;
     G = G > 8 ? 8 : G;
     blocks = (groups + 4 * G - 1) / (4 * G);
 }
