@@ -506,6 +506,33 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     const int C = seq_chunk(cnt);
     auto at = [&](int t) { return exact ? seq_idx(t, C) : t; };
     const float *ps = a.prob + (i * a.n_head + h) * a.span;
+    const size_t kv = (size_t)a.n_kv_head * HD;
+    const float *vb = a.v_cache + t0 * kv + (size_t)kvh * HD + d0;
+    constexpr int R4 = DB / 4;
+    // wave 0 adds the products; the waves that do not share its SIMD (waves
+    // are dealt to the 4 SIMDs in turn) form them, so the dependent adds
+    // issue back to back
+    constexpr int NPROD = (SEQ_T / 64 - SEQ_T / 256) * 64;
+    static_assert(CP * R4 == 2 * NPROD, "two float4 per producer thread per chunk");
+    // V loads run PD chunks ahead of the products (a register ring)
+    constexpr int PD = 8;
+    float4 ring[PD][2];
+    const int wv = tid >> 6;
+    const int pid = (wv & 3) ? (wv - (wv >> 2) - 1) * 64 + lane : -1;
+    auto issue = [&](float4 (&dst)[2], int c) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int idx = pid + k * NPROD;
+            const int t = c * CP + idx / R4;
+            dst[k] = t < cnt ? *(const float4 *)(vb + (size_t)t * kv + 4 * (idx % R4)) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    // the first PE chunks' V loads are in flight through the softmax (more
+    // would hold registers the exact sum needs), the rest of the ring after it
+    constexpr int PE = 2;
+    if (pid >= 0)
+#pragma unroll
+        for (int j = 0; j < PE; j++) issue(ring[j], j);
     ATT_TS(0);
     float mx = -INFINITY;
     for (int t = tid; t < cnt; t += SEQ_T) {
@@ -533,32 +560,11 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     for (int t = tid; t < cnt; t += SEQ_T) e[at(t)] = e[at(t)] * inv;
     __syncthreads();  // the sum's scratch is reused for the products below
     ATT_TS(3);
-    const size_t kv = (size_t)a.n_kv_head * HD;
-    const float *vb = a.v_cache + t0 * kv + (size_t)kvh * HD + d0;
-    constexpr int R4 = DB / 4;
-    // wave 0 adds the products; the waves that do not share its SIMD (waves
-    // are dealt to the 4 SIMDs in turn) form them, so the dependent adds
-    // issue back to back
-    constexpr int NPROD = (SEQ_T / 64 - SEQ_T / 256) * 64;
-    static_assert(CP * R4 == 2 * NPROD, "two float4 per producer thread per chunk");
-    // V loads run PD chunks ahead of the products (a register ring)
-    constexpr int PD = 8;
-    float4 ring[PD][2];
-    const int wv = tid >> 6;
-    const int pid = (wv & 3) ? (wv - (wv >> 2) - 1) * 64 + lane : -1;
-    auto issue = [&](float4 (&dst)[2], int c) {
-#pragma unroll
-        for (int k = 0; k < 2; k++) {
-            const int idx = pid + k * NPROD;
-            const int t = c * CP + idx / R4;
-            dst[k] = t < cnt ? *(const float4 *)(vb + (size_t)t * kv + 4 * (idx % R4)) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-    };
     float o = 0.0f;
     const int nch = (cnt + CP - 1) / CP;
     if (pid >= 0)
 #pragma unroll
-        for (int j = 0; j < PD; j++) issue(ring[j], j);
+        for (int j = PE; j < PD; j++) issue(ring[j], j);
     for (int c0 = 0; c0 < nch; c0 += PD) {
 #pragma unroll
         for (int j = 0; j < PD; j++) {
