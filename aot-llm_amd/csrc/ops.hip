@@ -10,6 +10,7 @@
 // int8 roundings downstream); transcendental functions are the host-libm
 // matched aotk_expf / aotk_tanhf. Maxima and integer sums use trees.
 #include "device.hpp"
+#include "lds_chain.hpp"
 #include "formats.hpp"
 #include "internal.hpp"
 #include "seqsum.hpp"
@@ -39,38 +40,52 @@ __device__ float block_sum(float v, float *red) {
     return t;
 }
 
-// Sequential f32 sum of n LDS values in index order, by one thread. Reads are
-// issued 32 values ahead of the dependent add chain so the chain runs at
-// VALU latency. n % 4 == 0, v 16-byte aligned.
+// Sequential f32 sum of n LDS values in index order, by one thread.
+// Plain sums run through lds_chain128 in runs of 128; the rest (and the sums
+// of squares) in groups of 32 that alternate between two register sets with
+// no copies between them: the reads of the next group are issued before the
+// adds of the current one (unconditionally: past the last full group they
+// re-read it). v 16-byte aligned.
 template <bool SQUARE>
 __device__ __forceinline__ float seq_sum_lds(const float *v, int n) {
     float s = 0.0f;
     int i = 0;
-    float4 cur[8];
-    int nfull = n / 32 * 32;
-    if (nfull > 0)
-        for (int k = 0; k < 8; k++) cur[k] = *(const float4 *)(v + 4 * k);
-    for (; i < nfull; i += 32) {
-        float4 nxt[8];
-        const bool more = i + 32 < nfull;
-        if (more)
-            for (int k = 0; k < 8; k++) nxt[k] = *(const float4 *)(v + i + 32 + 4 * k);
+    if (!SQUARE)
+        for (; i + 128 <= n; i += 128) s = lds_chain128(v + i, s);
+    const int nfull = i + (n - i) / 32 * 32;
+    auto add = [&](const float4 (&g)[8]) {
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             if (SQUARE) {
-                s += cur[k].x * cur[k].x;
-                s += cur[k].y * cur[k].y;
-                s += cur[k].z * cur[k].z;
-                s += cur[k].w * cur[k].w;
+                s += g[k].x * g[k].x;
+                s += g[k].y * g[k].y;
+                s += g[k].z * g[k].z;
+                s += g[k].w * g[k].w;
             } else {
-                s += cur[k].x;
-                s += cur[k].y;
-                s += cur[k].z;
-                s += cur[k].w;
+                s += g[k].x;
+                s += g[k].y;
+                s += g[k].z;
+                s += g[k].w;
             }
         }
-        if (more)
-            for (int k = 0; k < 8; k++) cur[k] = nxt[k];
+    };
+    if (nfull > i) {
+        const int last = nfull - 32;
+        float4 a[8], b[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) a[k] = *(const float4 *)(v + i + 4 * k);
+        for (;;) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) b[k] = *(const float4 *)(v + min(i + 32, last) + 4 * k);
+            add(a);
+            i += 32;
+            if (i >= nfull) break;
+#pragma unroll
+            for (int k = 0; k < 8; k++) a[k] = *(const float4 *)(v + min(i + 32, last) + 4 * k);
+            add(b);
+            i += 32;
+            if (i >= nfull) break;
+        }
     }
     for (; i < n; i++) s += SQUARE ? v[i] * v[i] : v[i];
     return s;
@@ -513,6 +528,7 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     // are dealt to the 4 SIMDs in turn) form them, so the dependent adds
     // issue back to back
     constexpr int NPROD = (SEQ_T / 64 - SEQ_T / 256) * 64;
+    static_assert(CP == 192, "the output adds of a full chunk run in lds_chain192");
     static_assert(CP * R4 == 2 * NPROD, "two float4 per producer thread per chunk");
     // V loads run PD chunks ahead of the products (a register ring)
     constexpr int PD = 8;
@@ -591,33 +607,10 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
                 __syncthreads();
                 SV_TS(c, 1);
                 if (tid < DB) {
-                    // groups of 16 in two register sets, each set loaded one
-                    // group ahead of its adds
-                    const float4 *bp = (const float4 *)(buf + tid * SV_RS);
-                    int full = rows & ~31;
-                    float4 ga[4], gb[4];
-#pragma unroll
-                    for (int k = 0; k < 4; k++) ga[k] = bp[k];
-                    for (int r = 0; r < full; r += 32) {
-#pragma unroll
-                        for (int k = 0; k < 4; k++) gb[k] = bp[r / 4 + 4 + k];
-#pragma unroll
-                        for (int k = 0; k < 4; k++) {
-                            o += ga[k].x; o += ga[k].y; o += ga[k].z; o += ga[k].w;
-                        }
-#pragma unroll
-                        for (int k = 0; k < 4; k++) ga[k] = bp[r / 4 + 8 + k];  // past the end on the last group: unused
-#pragma unroll
-                        for (int k = 0; k < 4; k++) {
-                            o += gb[k].x; o += gb[k].y; o += gb[k].z; o += gb[k].w;
-                        }
-                    }
-                    if (rows - full >= 16) {  // ga holds the group at `full`
-#pragma unroll
-                        for (int k = 0; k < 4; k++) {
-                            o += ga[k].x; o += ga[k].y; o += ga[k].z; o += ga[k].w;
-                        }
-                        full += 16;
+                    int full = 0;
+                    if (rows == CP) {
+                        o = lds_chain192(buf + tid * SV_RS, o);
+                        full = CP;
                     }
                     const float *tp = buf + tid * SV_RS;
                     for (int r = full; r < rows; r++) o += tp[r];
