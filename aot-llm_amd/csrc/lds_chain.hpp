@@ -59,6 +59,16 @@ namespace aotk {
 
 __device__ __forceinline__ uint32_t lds_addr(const float *p) { return (uint32_t)(uintptr_t)p; }
 
+// s + p[0..63] in order (p in LDS, 16-byte aligned).
+__device__ __forceinline__ float lds_chain64(const float *p, float s) {
+    uint32_t ad = lds_addr(p);
+    asm volatile(LC_PRO LC_RA LC_RB LC_RA LC_FB
+                 : [o] "+v"(s), [ad] "+v"(ad)
+                 :
+                 : "memory", LC_CLOBBER);
+    return s;
+}
+
 // s + p[0..127] in order (p in LDS, 16-byte aligned).
 __device__ __forceinline__ float lds_chain128(const float *p, float s) {
     uint32_t ad = lds_addr(p);

@@ -426,6 +426,21 @@ __global__ __launch_bounds__(576) void k_attn_qk_decode(AttnArgs a, QkvPost p) {
     const int rows = (int)min((size_t)ATT_CH, n - start);
     const size_t kv = (size_t)a.n_kv_head * HD;
     const float *cs_row = p.cs + pos * p.rot_dim;
+    // the chunk's K rows do not depend on the epilogue: the first PK float4
+    // of each thread are loaded before it (the new position's row is filled
+    // from the post-processed k below)
+    const float *kb = a.k_cache + start * kv + (size_t)kvh * HD;
+    constexpr int R4 = HD / 4;
+    constexpr int PK = 8;
+    const int nthreads = (gqa + 1) * 64;
+    float4 kpre[PK];
+#pragma unroll
+    for (int j = 0; j < PK; j++) {
+        const int idx = threadIdx.x + j * nthreads;
+        const int r = idx / R4, c4 = idx % R4;
+        kpre[j] = idx < rows * R4 && start + r != pos ? *(const float4 *)(kb + (size_t)r * kv + 4 * c4)
+                                                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
     if (hg < gqa) {
         const int h = kvh * gqa + hg;
         head_post_wave(sq[hg], p.q + (size_t)h * HD, p.bq ? p.bq + (size_t)h * HD : nullptr, p.q_norm, cs_row, HD,
@@ -445,11 +460,20 @@ __global__ __launch_bounds__(576) void k_attn_qk_decode(AttnArgs a, QkvPost p) {
             }
         }
     }
-    // K rows of the chunk (the new position from the post-processed k)
-    const float *kb = a.k_cache + start * kv + (size_t)kvh * HD;
-    constexpr int R4 = HD / 4;
-    const int nthreads = (gqa + 1) * 64;
-    for (int idx = threadIdx.x; idx < rows * R4; idx += nthreads) {
+    // K rows of the chunk into LDS (the new position from the post-processed k)
+#pragma unroll
+    for (int j = 0; j < PK; j++) {
+        const int idx = threadIdx.x + j * nthreads;
+        if (idx < rows * R4) {
+            const int r = idx / R4, c4 = idx % R4;
+            float *d = sk + r * KS + 4 * c4;
+            d[0] = kpre[j].x;
+            d[1] = kpre[j].y;
+            d[2] = kpre[j].z;
+            d[3] = kpre[j].w;
+        }
+    }
+    for (int idx = threadIdx.x + PK * nthreads; idx < rows * R4; idx += nthreads) {
         const int r = idx / R4, c4 = idx % R4;
         float4 k4;
         if (start + r == pos) k4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -594,12 +618,14 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
                     for (int k = 0; k < 2; k++) {
                         const int idx = pid + k * NPROD;
                         const int r = idx / R4, d = 4 * (idx % R4);
-                        const float pt = r < rows ? e[at(base + r)] : 0.0f;
+                        // rows past the span hold -0.0, which leaves any sum unchanged
+                        const bool in = r < rows;
+                        const float pt = in ? e[at(base + r)] : 0.0f;
                         const float4 v4 = ring[j][k];
-                        buf[(d + 0) * SV_RS + r] = pt * v4.x;
-                        buf[(d + 1) * SV_RS + r] = pt * v4.y;
-                        buf[(d + 2) * SV_RS + r] = pt * v4.z;
-                        buf[(d + 3) * SV_RS + r] = pt * v4.w;
+                        buf[(d + 0) * SV_RS + r] = in ? pt * v4.x : -0.0f;
+                        buf[(d + 1) * SV_RS + r] = in ? pt * v4.y : -0.0f;
+                        buf[(d + 2) * SV_RS + r] = in ? pt * v4.z : -0.0f;
+                        buf[(d + 3) * SV_RS + r] = in ? pt * v4.w : -0.0f;
                     }
                     issue(ring[j], c + PD);
                 }
@@ -607,13 +633,11 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
                 __syncthreads();
                 SV_TS(c, 1);
                 if (tid < DB) {
-                    int full = 0;
-                    if (rows == CP) {
-                        o = lds_chain192(buf + tid * SV_RS, o);
-                        full = CP;
-                    }
+                    // the chunk's rows rounded up to 64 (the padding adds -0.0)
                     const float *tp = buf + tid * SV_RS;
-                    for (int r = full; r < rows; r++) o += tp[r];
+                    if (rows > 128) o = lds_chain192(tp, o);
+                    else if (rows > 64) o = lds_chain128(tp, o);
+                    else o = lds_chain64(tp, o);
                 }
                 SV_TS(c, 2);
             }
