@@ -91,6 +91,17 @@ __device__ __forceinline__ float seq_sum_lds(const float *v, int n) {
     return s;
 }
 
+// The same for v padded with -0.0 up to a multiple of 64 values: whole
+// runs of the assembly chain.
+__device__ __forceinline__ float seq_sum_lds_pad64(const float *v, int n) {
+    const int n64 = (n + 63) & ~63;
+    float s = 0.0f;
+    int i = 0;
+    for (; i + 128 <= n64; i += 128) s = lds_chain128(v + i, s);
+    if (i < n64) s = lds_chain64(v + i, s);
+    return s;
+}
+
 // ss = sum of v*v over n values in LDS, in index order (ops.rs:10-13). Run
 // by one thread; the result is broadcast through LDS.
 __device__ float seq_sumsq_lds(const float *v, int n, float *bcast) {
@@ -586,13 +597,16 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     mx = wave_max(lane < SEQ_T / 64 ? red[lane] : -INFINITY);
     ATT_TS(1);
     for (int t = tid; t < cnt; t += SEQ_T) e[at(t)] = aotk_expf(e[at(t)] - mx);
+    // the one-thread sum runs over whole runs of 64: the positions past the
+    // span up to the next multiple of 64 hold -0.0, which leaves it unchanged
+    if (!exact && tid < 64 && cnt + tid < ((cnt + 63) & ~63)) e[cnt + tid] = -0.0f;
     __syncthreads();
     ATT_TS(2);
     float sum;
     if (exact) {
         sum = exact_seq_sum(e, cnt, S);
     } else {
-        if (tid == 0) bc = seq_sum_lds<false>(e, cnt);
+        if (tid == 0) bc = seq_sum_lds_pad64(e, cnt);
         __syncthreads();
         sum = bc;
     }
@@ -678,9 +692,10 @@ __global__ __launch_bounds__(256) void k_attn_softmax_rows(AttnArgs a, int m) {
     }
     mx = wave_max(mx);
     for (int t = lane; t < cnt; t += 64) ew[t] = aotk_expf(ew[t] - mx);
+    if (cnt + lane < ((cnt + 63) & ~63)) ew[cnt + lane] = -0.0f;  // neutral padding to a run of 64
     wave_lds_sync();
     float sum = 0.0f;
-    if (lane == 0) sum = seq_sum_lds<false>(ew, cnt);
+    if (lane == 0) sum = seq_sum_lds_pad64(ew, cnt);
     const float inv = 1.0f / readlane_f(sum, 0);
     for (int t = lane; t < cnt; t += 64) ps[t] = ew[t] * inv;
 }
