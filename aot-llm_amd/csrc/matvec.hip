@@ -1020,8 +1020,10 @@ struct Q8bW {
 template <int KIND>
 __global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
     constexpr int R = Q8B_R;
-    __shared__ __align__(16) int8_t sy[Q8B_MAX_COLS];
-    __shared__ float syd[Q8B_MAX_COLS / 32];
+    // the activation (cols int8 quants, then cols / 32 scales), sized by the
+    // launch so that short rows leave LDS for more blocks per CU
+    extern __shared__ __align__(16) int8_t sy[];
+    float *syd = (float *)(sy + a.cols);
     __shared__ float sP[4][R * Q8B_PS];
     __shared__ float sD[4][R][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1332,6 +1334,8 @@ static bool mv_half_fits(const MvArgs &a) {
 
 // ----------------------------------------------------------------- launch
 
+static size_t q8b_lds(const MvArgs &a) { return a.cols + a.cols / 32 * sizeof(float); }
+
 static MvArgs make_args(int n, const DevWeight *const ws[], float *const ys[], const float *const adds[], const void *x_act) {
     MvArgs a = {};
     const DevWeight &w0 = *ws[0];
@@ -1452,7 +1456,7 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
     case AOTK_Q8_0:
         if (a.cols <= (size_t)Q8B_MAX_COLS) {
             grid.x = (unsigned)((a.total_rows + 4 * Q8B_R - 1) / (4 * Q8B_R));
-            k_mv_q8b<AOTK_Q8_0><<<grid, 256, 0, s>>>(a);
+            k_mv_q8b<AOTK_Q8_0><<<grid, 256, q8b_lds(a), s>>>(a);
         } else {
             grid.x = (unsigned)((a.total_rows + 31) / 32);
             k_mv_q80<AOTK_Q8_0><<<grid, 256, 0, s>>>(a);
@@ -1461,7 +1465,7 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
     case AOTK_Q4_0:
         if (a.cols <= (size_t)Q8B_MAX_COLS) {
             grid.x = (unsigned)((a.total_rows + 4 * Q8B_R - 1) / (4 * Q8B_R));
-            k_mv_q8b<AOTK_Q4_0><<<grid, 256, 0, s>>>(a);
+            k_mv_q8b<AOTK_Q4_0><<<grid, 256, q8b_lds(a), s>>>(a);
         } else {
             grid.x = (unsigned)((a.total_rows + 31) / 32);
             k_mv_q80<AOTK_Q4_0><<<grid, 256, 0, s>>>(a);
@@ -1470,7 +1474,7 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
     case AOTK_Q5_0:
         if (a.cols <= (size_t)Q8B_MAX_COLS) {
             grid.x = (unsigned)((a.total_rows + 4 * Q8B_R - 1) / (4 * Q8B_R));
-            k_mv_q8b<AOTK_Q5_0><<<grid, 256, 0, s>>>(a);
+            k_mv_q8b<AOTK_Q5_0><<<grid, 256, q8b_lds(a), s>>>(a);
         } else {
             grid.x = (unsigned)((a.total_rows + 31) / 32);
             k_mv_q80<AOTK_Q5_0><<<grid, 256, 0, s>>>(a);
