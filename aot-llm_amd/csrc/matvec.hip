@@ -1057,18 +1057,33 @@ __global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
             w[r].d = wd[r][b];
         }
     };
+    // the activation's loads first (cols <= 16384: at most 4 quads and one
+    // scale per thread, indices past the end re-read the last), then the
+    // first two steps' weights: the wait for the activation leaves those in
+    // flight
+    const uint4 *xq = (const uint4 *)(a.xq + (size_t)tok * a.cols);
+    const int nq = (int)(a.cols / 16);
+    uint4 xv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) xv[k] = xq[min(tid + 256 * k, nq - 1)];
+    float xdv[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) xdv[k] = a.xd[(size_t)tok * nb + min(tid + 256 * k, nb - 1)];
     Q8bW<KIND> cur[R], nxt[R];
     load(cur, 0);
-    {
-        const uint4 *xq = (const uint4 *)(a.xq + (size_t)tok * a.cols);
-        for (int i = tid; i < (int)(a.cols / 16); i += 256) ((uint4 *)sy)[i] = xq[i];
-        for (int i = tid; i < nb; i += 256) syd[i] = a.xd[(size_t)tok * nb + i];
-    }
+    load(nxt, 64);
+    // (unconditional stores: past the end they repeat the last element's
+    // value at its own place, which keeps the loads above unconditional too)
+#pragma unroll
+    for (int k = 0; k < 4; k++) ((uint4 *)sy)[min(tid + 256 * k, nq - 1)] = xv[k];
+#pragma unroll
+    for (int k = 0; k < 2; k++) syd[min(tid + 256 * k, nb - 1)] = xdv[k];
     __syncthreads();
     const int rr = lane >> 3, chain = lane & 7;
     float acc = 0.0f;
-    for (int c0 = 0; c0 < nb; c0 += 64) {
-        if (c0 + 64 < nb) load(nxt, c0 + 64);
+    // one step of 64 blocks: phase A (the integer sums and scales into LDS),
+    // phase B (the chains)
+    auto step = [&](const Q8bW<KIND> (&w)[R], int c0) {
         // phase A
         const int b = c0 + lane;
         if (b < nb) {
@@ -1083,17 +1098,17 @@ __global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
             for (int r = 0; r < R; r++) {
                 float P[8];
                 if (KIND == AOTK_Q8_0) {
-                    const uint32_t ww[8] = {cur[r].w0.x, cur[r].w0.y, cur[r].w0.z, cur[r].w0.w,
-                                            cur[r].w1.x, cur[r].w1.y, cur[r].w1.z, cur[r].w1.w};
+                    const uint32_t ww[8] = {w[r].w0.x, w[r].w0.y, w[r].w0.z, w[r].w0.w,
+                                            w[r].w1.x, w[r].w1.y, w[r].w1.z, w[r].w1.w};
 #pragma unroll
                     for (int l = 0; l < 8; l++) P[l] = (float)dot4(ww[l], yw[l], 0);
                 } else {
-                    const uint32_t nw[4] = {cur[r].w0.x, cur[r].w0.y, cur[r].w0.z, cur[r].w0.w};
+                    const uint32_t nw[4] = {w[r].w0.x, w[r].w0.y, w[r].w0.z, w[r].w0.w};
 #pragma unroll
                     for (int l = 0; l < 8; l++) {
                         uint32_t v = l < 4 ? (nw[l] & 0x0F0F0F0Fu) : ((nw[l - 4] >> 4) & 0x0F0F0F0Fu);
                         if (KIND == AOTK_Q5_0) {
-                            const uint32_t b4 = (cur[r].qh >> (4 * l)) & 0xFu;
+                            const uint32_t b4 = (w[r].qh >> (4 * l)) & 0xFu;
                             const uint32_t spread = (b4 & 1u) | ((b4 & 2u) << 7) | ((b4 & 4u) << 14) | ((b4 & 8u) << 21);
                             v |= spread << 4;
                         }
@@ -1103,7 +1118,7 @@ __global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
                 float *dst = &sP[wave][r * Q8B_PS + lane * 9];
 #pragma unroll
                 for (int l = 0; l < 8; l++) dst[l] = P[l];
-                sD[wave][r][lane] = f16_to_f32(cur[r].d) * yd;
+                sD[wave][r][lane] = f16_to_f32(w[r].d) * yd;
             }
         }
         wave_lds_sync();
@@ -1126,9 +1141,15 @@ __global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
             for (; i < n; i++) acc = fmaf(dp[i], pp[i * 9], acc);
         }
         wave_lds_sync();
-        if (c0 + 64 < nb)
-#pragma unroll
-            for (int r = 0; r < R; r++) cur[r] = nxt[r];
+    };
+    // two register sets in turn, no copies; every load is unconditional
+    // (steps past the end re-read the last block), so the waits stay exact
+    for (int c0 = 0; c0 < nb; c0 += 128) {
+        step(cur, c0);
+        load(cur, c0 + 128);
+        if (c0 + 64 >= nb) break;
+        step(nxt, c0 + 64);
+        load(nxt, c0 + 192);
     }
     // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7))  (simd_avx2.rs:27-34)
     const float t = acc + shfl_xor(acc, 4);
