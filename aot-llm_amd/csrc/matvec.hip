@@ -49,17 +49,13 @@ struct MvArgs {
 // Segment of a global row (constant indices only, so that the kernel
 // arguments stay in scalar registers).
 __device__ __forceinline__ int seg_of(const MvArgs &a, int row, int &local) {
+    // selects, not branches: loads whose addresses depend on it stay in one
+    // basic block, so the waits for them can stay exact
     const int r0 = a.rows[0], r1 = a.rows[1];
-    if (a.nseg > 1 && row >= r0) {
-        if (a.nseg > 2 && row >= r0 + r1) {
-            local = row - r0 - r1;
-            return 2;
-        }
-        local = row - r0;
-        return 1;
-    }
-    local = row;
-    return 0;
+    const bool s1 = a.nseg > 1 && row >= r0;
+    const bool s2 = a.nseg > 2 && row >= r0 + r1;
+    local = row - (s2 ? r0 + r1 : (s1 ? r0 : 0));
+    return s2 ? 2 : (s1 ? 1 : 0);
 }
 template <typename T>
 __device__ __forceinline__ T seg_sel(int s, T v0, T v1, T v2) { return s == 0 ? v0 : (s == 1 ? v1 : v2); }
@@ -416,12 +412,13 @@ __device__ __forceinline__ float kq_term(const uint4 (&c)[kq_chl<KIND, SPL>()], 
 // instantiation up to 32 super-blocks, else one.
 __host__ __device__ constexpr int kq_spl(int nb) { return nb > 0 && nb <= 32 ? 2 : 1; }
 
-// PF = 0: one row group per wave (G == 1), register budget for 4 waves per
-// SIMD; PF = 1: G groups per wave with the next group's loads in flight.
+// PF = 1: G groups per wave with the next group's loads in flight while the
+// current one computes; PF = 2: the same for G >= 2, with the second group's
+// loads issued together with the first's.
 // NB > 0: the super-blocks per row as a compile-time constant (immediate
 // chunk offsets, constant row-slot division, an unmasked fold); NB == 0 reads
 // it from the arguments.
-template <int KIND, int PF, int NB>
+template <int KIND, int PF, int NB, bool QSRC = false>
 __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int bx, uint8_t *sY, float (*sT)[256 + 16]) {
     using Geo = KqGeom<KIND>;
     constexpr int SPL = kq_spl(NB);
@@ -456,15 +453,47 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
             d6 = f16_to_f32(((const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]))[(size_t)local * nb + sa]);
     };
     MV_TS(0);
-    load(cur, dcur, 0);  // weights first: the longest latency
-    // stage this token's Q8_K activation in LDS
-    if (a.xq_src) {
+    // This token's Q8_K activation is loaded first (<= 64 super-blocks: four
+    // quads of qs, one of bsums and one scale per thread; indices past the
+    // end repeat the last element), then the weights of the first group (and
+    // with PF == 2 of the second): waiting for the activation then leaves
+    // the weights in flight.
+    constexpr bool stage = !QSRC;  // QSRC: the input arrives in f32 (a.xq_src) and is quantized here
+    const int nq = nb * 16;
+    uint4 xv[4], bv;
+    float dv;
+    float4 xf[4];  // the f32 input of the wave's first four super-blocks, when it quantizes
+    if constexpr (stage) {
+        const uint4 *xq = (const uint4 *)(a.xq + (size_t)tok * a.cols);
+        const uint4 *xb = (const uint4 *)(a.xbs + (size_t)tok * nb * 16);
+#pragma unroll
+        for (int k = 0; k < 4; k++) xv[k] = xq[min(tid + 256 * k, nq - 1)];
+        bv = xb[min(tid, 2 * nb - 1)];
+        dv = a.xd[(size_t)tok * nb + min(tid, nb - 1)];
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; k++) xf[k] = ((const float4 *)(a.xq_src + (size_t)min(wave + 4 * k, nb - 1) * 256))[lane];
+    }
+    load(cur, dcur, 0);
+    if (PF == 2) load(nxt, dnxt, 1);  // G >= 2
+    if constexpr (stage) {
+        // unconditional stores: past the end they repeat the last element
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = min(tid + 256 * k, nq - 1);
+            *(uint4 *)(sY + (i >> 4) * KQ_REC + (i & 15) * 16) = xv[k];
+        }
+        const int ib = min(tid, 2 * nb - 1);
+        *(uint4 *)(sY + (ib >> 1) * KQ_REC + 256 + (ib & 1) * 16) = bv;
+        *(float *)(sY + min(tid, nb - 1) * KQ_REC + 288) = dv;
+    } else {
         // quantize the f32 input here, wave w taking super-blocks w, w + 4,
         // ... (the device quantizer of k_quant_f32, quant.rs:248-283)
         for (int b0 = wave; b0 < nb; b0 += 16) {
-            float4 v4[4];  // four super-blocks' loads in flight together
+            float4 v4[4];  // four super-blocks' loads in flight together (the first four loaded above)
 #pragma unroll
-            for (int k = 0; k < 4; k++) v4[k] = ((const float4 *)(a.xq_src + (size_t)min(b0 + 4 * k, nb - 1) * 256))[lane];
+            for (int k = 0; k < 4; k++)
+                v4[k] = b0 == wave ? xf[k] : ((const float4 *)(a.xq_src + (size_t)min(b0 + 4 * k, nb - 1) * 256))[lane];
             Q8KLane rq[4];  // independent: their reductions interleave
 #pragma unroll
             for (int k = 0; k < 4; k++) {
@@ -482,12 +511,6 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
                 if (lane == 0) *(float *)(recb + 288) = r.d;
             }
         }
-    } else {
-        const uint4 *xq = (const uint4 *)(a.xq + (size_t)tok * a.cols);
-        for (int i = tid; i < nb * 16; i += 256) *(uint4 *)(sY + (i >> 4) * KQ_REC + (i & 15) * 16) = xq[i];
-        const uint4 *xb = (const uint4 *)(a.xbs + (size_t)tok * nb * 16);
-        for (int i = tid; i < nb * 2; i += 256) *(uint4 *)(sY + (i >> 1) * KQ_REC + 256 + (i & 1) * 16) = xb[i];
-        for (int i = tid; i < nb; i += 256) *(float *)(sY + i * KQ_REC + 288) = a.xd[(size_t)tok * nb + i];
     }
     __syncthreads();
     MV_TS(1);
@@ -527,7 +550,7 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
     // groups alternate between the two register buffers (no copies)
     for (int gi = 0; gi < ng; gi += 2) {
         if ((group0 + gi) * RL >= a.total_rows) break;
-        if (PF && gi + 1 < ng) load(nxt, dnxt, gi + 1);
+        if (PF && gi + 1 < ng && !(PF == 2 && gi == 0)) load(nxt, dnxt, gi + 1);
         group(cur, dcur, gi);
         if (!PF || gi + 1 >= ng || (group0 + gi + 1) * RL >= a.total_rows) break;
         if (gi + 2 < ng) load(cur, dcur, gi + 2);
@@ -541,10 +564,10 @@ struct KqShared {
     __align__(16) float t[4][256 + 16];  // [wave][row slot * ts + super-block] (+ read slack)
 };
 
-template <int KIND, int PF, int NB>
+template <int KIND, int PF, int NB, bool QSRC = false>
 __global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq(MvArgs a, int RL, int G) {
     __shared__ KqShared sh;
-    mv_kq_body<KIND, PF, NB>(a, RL, G, blockIdx.x, sh.y, sh.t);
+    mv_kq_body<KIND, PF, NB, QSRC>(a, RL, G, blockIdx.x, sh.y, sh.t);
 }
 
 // Two K-quant matrices of different kinds sharing the input in one launch
@@ -1415,9 +1438,19 @@ static void launch_kq(const MvArgs &a, dim3 grid, hipStream_t s) {
         int RL, G, blocks;
         kq_shape(a, RL, G, blocks);
         grid.x = (unsigned)blocks;
-#define F(NB) k_mv_kq<KIND, 1, NB><<<grid, 256, 0, s>>>(a, RL, G)
-        AOTK_NB_SWITCH(a.nb, F)
+        if (a.xq_src) {
+#define F(NB) k_mv_kq<KIND, 1, NB, true><<<grid, 256, 0, s>>>(a, RL, G)
+            AOTK_NB_SWITCH(a.nb, F)
 #undef F
+        } else if (G >= 2) {
+#define F(NB) k_mv_kq<KIND, 2, NB><<<grid, 256, 0, s>>>(a, RL, G)
+            AOTK_NB_SWITCH(a.nb, F)
+#undef F
+        } else {
+#define F(NB) k_mv_kq<KIND, 1, NB><<<grid, 256, 0, s>>>(a, RL, G)
+            AOTK_NB_SWITCH(a.nb, F)
+#undef F
+        }
     } else {
         grid.x = (unsigned)((a.total_rows + 7) / 8);
         k_mv_kquant<KIND, 2><<<grid, 256, 0, s>>>(a);
