@@ -702,8 +702,11 @@ __global__ __launch_bounds__(256) void k_attn_softmax_rows(AttnArgs a, int m) {
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_out_rows(AttnArgs a, int m) {
+    static_assert(ATT_RB == 4, "one float4 of p per position");
+    __shared__ float4 sPr[4][32];
     constexpr int NS = HD / 64;
     const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
     const int task = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int slice = task % NS, h = (task / NS) % a.n_head, rg = task / (NS * a.n_head);
     if (rg * ATT_RB >= m) return;
@@ -740,9 +743,12 @@ __global__ __launch_bounds__(256) void k_attn_out_rows(AttnArgs a, int m) {
         for (size_t t = lo; t < alo; t++) step_if(t);
         // groups of 32 positions in two register sets (A, B), each loaded one
         // group ahead of its use: V with one load per position, p with one
-        // load per row (lane k holds position k) broadcast by readlane
+        // load per row (lane k holds position k), written to this wave's LDS
+        // slot as [position][row] so that one broadcast 16-byte read gives
+        // the four rows' p of a position
         size_t t = alo;
         float va[32], pa[ATT_RB], vbb[32], pb[ATT_RB];
+        float4 *sp = sPr[wv];
         auto load = [&](float (&v)[32], float (&pv)[ATT_RB], size_t c) {
 #pragma unroll
             for (int k = 0; k < 32; k++) v[k] = vb[(c + k) * kv];
@@ -750,10 +756,17 @@ __global__ __launch_bounds__(256) void k_attn_out_rows(AttnArgs a, int m) {
             for (int r = 0; r < ATT_RB; r++) pv[r] = pr[r][c + (lane & 31)];
         };
         auto use = [&](const float (&v)[32], const float (&pv)[ATT_RB]) {
+            if (lane < 32) sp[lane] = make_float4(pv[0], pv[1], pv[2], pv[3]);
+            wave_lds_sync();
 #pragma unroll
-            for (int k = 0; k < 32; k++)
-#pragma unroll
-                for (int r = 0; r < ATT_RB; r++) o[r] += readlane_f(pv[r], k) * v[k];
+            for (int k = 0; k < 32; k++) {
+                const float4 p4 = sp[k];
+                o[0] += p4.x * v[k];
+                o[1] += p4.y * v[k];
+                o[2] += p4.z * v[k];
+                o[3] += p4.w * v[k];
+            }
+            wave_lds_sync();
         };
         if (t + 32 <= ahi) load(va, pa, t);
         while (t + 32 <= ahi) {
