@@ -941,6 +941,98 @@ __global__ __launch_bounds__(256) void k_mm_ks(MvArgs a, int m) {
     }
 }
 
+// Prompt matmul, all tokens (m <= 64) in one block of 16 weight rows: the
+// 4 waves split the super-blocks (wave w: w, w + 4, ...) and each runs all
+// the token tiles of its super-block in turn, so a super-block's B
+// fragments are unpacked once for up to 64 tokens (mm_sb_terms per tile on
+// the same weights: the unpacking is common to the calls and computed
+// once). A tile's activation (16 tokens x 256 bytes) is staged in the
+// wave's LDS, the next tile's (or the next super-block's first) loads in
+// flight meanwhile. Per round the four super-blocks' terms meet in LDS and
+// wave t adds those of tile t in super-block order (the matvec fold).
+template <int KIND>
+__global__ __launch_bounds__(256) void k_mm_kt(MvArgs a, int m) {
+    __shared__ __align__(16) uint8_t sY[4][2][16 * MM_YS];
+    __shared__ float sD[4][2][16];
+    __shared__ float sT[4][4][4][64];  // [slot][tile][i][lane]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, r16 = lane & 15;
+    const int nb = a.nb;
+    const int grow = blockIdx.x * 16 + r16;
+    const int mt = min(64, m);
+    const int ntiles = (mt + 15) / 16;
+    const bool row_ok = grow < a.total_rows;
+    int local;
+    const int sg = seg_of(a, row_ok ? grow : 0, local);
+    const uint8_t *rowp = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * nb * KqGeom<KIND>::RB;
+    const uint16_t *drow = KIND == AOTK_Q6_K ? (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb : nullptr;
+    struct Stg {
+        uint4 v[4];  // 16 tokens x 16 uint4
+        float d;
+    };
+    auto stage_load = [&](Stg &r, int sb, int t) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int idx = lane + 64 * k;
+            const int tk = 16 * t + (idx >> 4), c = idx & 15;
+            r.v[k] = tk < mt ? *(const uint4 *)(a.xq + (size_t)tk * a.cols + (size_t)sb * 256 + 16 * c) : make_uint4(0, 0, 0, 0);
+        }
+        const int tk = 16 * t + lane;
+        r.d = lane < 16 && tk < mt ? a.xd[(size_t)tk * nb + sb] : 0.0f;
+    };
+    auto stage_store = [&](const Stg &r, int buf) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int idx = lane + 64 * k;
+            *(uint4 *)(sY[wave][buf] + (idx >> 4) * MM_YS + 16 * (idx & 15)) = r.v[k];
+        }
+        if (lane < 16) sD[wave][buf][lane] = r.d;
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // waves < ntiles: tile `wave`
+    const int rounds = (nb + 3) / 4;
+    MmW<KIND> cur, nxt;
+    Stg st;
+    if (wave < nb) {
+        mm_load<KIND>(cur, rowp, drow, wave, nb, q);
+        stage_load(st, wave, 0);
+    }
+    for (int r = 0; r < rounds; r++) {
+        const int sb = 4 * r + wave;
+        if (sb < nb) {
+            if (sb + 4 < nb) mm_load<KIND>(nxt, rowp, drow, sb + 4, nb, q);
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                if (t >= ntiles) break;
+                stage_store(st, t & 1);
+                wave_lds_sync();
+                if (t + 1 < ntiles) stage_load(st, sb, t + 1);
+                else if (sb + 4 < nb) stage_load(st, sb + 4, 0);
+                float term[1][4];
+                mm_sb_terms<KIND, 1>(cur, sY[wave][t & 1], sD[wave][t & 1], q, r16, mt - 16 * t, term);
+#pragma unroll
+                for (int i = 0; i < 4; i++) sT[wave][t][i][lane] = term[0][i];
+            }
+            if (sb + 4 < nb) cur = nxt;
+        }
+        __syncthreads();
+        if (wave < ntiles) {
+            const int n = min(4, nb - 4 * r);
+            for (int slot = 0; slot < n; slot++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i] = acc[i] + sT[slot][wave][i][lane];
+        }
+        __syncthreads();
+    }
+    if (wave < ntiles && row_ok) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int tk = 16 * wave + 4 * q + i;
+            if (tk < mt) store_row(a, grow, tk, acc[i]);
+        }
+    }
+}
+
 // ------------------------------------------------------ Q8_0 / Q4_0 / Q5_0
 // Wave = 8 rows. Phase A: lanes turn 32 blocks of 2 rows per pass into the 8
 // per-lane integer sums P and the scale D = f16(d) * y.d, staged in LDS.
@@ -1470,6 +1562,21 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
         // Q6_K down slightly faster, 4096-row Q4_K wo slightly slower):
         // super-blocks split over the waves
         const unsigned cells = rb * (unsigned)tiles;
+        // 2048 rows or more: the whole batch per 16-row block, super-blocks
+        // split over the waves (measured at 64 tokens: the 4096-row Q6_K
+        // down 82 -> 69 us, the 4096/5120-row Q4_K wo and q/k 20/24 -> 19/22
+        // us, the 28672-row gate/up unchanged); fewer rows leave too few
+        // blocks (the 1024-row v: 12 -> 21 us) and keep the kernels below
+        static const bool kt_off = getenv("AOTK_NO_MM_KT") != nullptr;
+        if (a.total_rows >= 2048 && !kt_off) {
+            dim3 gk((unsigned)((a.total_rows + 15) / 16), 1);
+            switch (kind) {
+            case AOTK_Q4_K: k_mm_kt<AOTK_Q4_K><<<gk, 256, 0, s>>>(a, (int)m); break;
+            case AOTK_Q5_K: k_mm_kt<AOTK_Q5_K><<<gk, 256, 0, s>>>(a, (int)m); break;
+            default: k_mm_kt<AOTK_Q6_K><<<gk, 256, 0, s>>>(a, (int)m); break;
+            }
+            return;
+        }
         if (cells < 128 || (cells <= 256 && a.nb >= 32)) {
             dim3 gk((unsigned)((a.total_rows + 15) / 16), (unsigned)tiles);
             switch (kind) {

@@ -108,6 +108,22 @@ def test_matmul_equals_matvec(aotk, oracle, kind):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("kind", [Q4_K, Q5_K, Q6_K], ids=lambda k: NAMES[k])
+def test_matmul_many_rows(aotk, oracle, kind):
+    """2048 rows or more take the whole batch per 16-row block (super-blocks
+    split over the waves): ragged row and token counts, a tile boundary."""
+    rng = np.random.default_rng(17)
+    cols, rows = 1280, 2100
+    raw = weights(kind, rows, cols, 9, oracle)
+    w = aotk.Weight(kind, raw, rows, cols)
+    for m in (2, 17, 64):
+        xs = [(rng.standard_normal(cols)).astype(np.float32) for _ in range(m)]
+        acts = np.concatenate([oracle.quantize_act(kind, x) for x in xs])
+        got = aotk.matmul(w, acts, m)
+        ref = oracle.matmul(kind, raw, acts, m, rows, cols).reshape(m, rows)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), m
+
+
 def test_rope_bitexact(aotk, oracle):
     rng = np.random.default_rng(9)
     for neox in (0, 1):
