@@ -383,6 +383,72 @@ __global__ __launch_bounds__(512) void k_attn_scores(AttnArgs a) {
     a.prob[(i * a.n_head + (size_t)(kvh * gqa + hg)) * a.span + (start + lane - t0)] = s * a.scale;
 }
 
+// Prompt scores for ATT_SRB rows per block: block = (kv head, chunk of
+// ATT_CH absolute positions, group of ATT_SRB rows), gqa * 64 threads. The
+// chunk's K rows are staged once for the group; thread (query head,
+// position) runs the rows' dot products side by side, each sequentially over
+// the head dimension, and writes those of the rows whose range [t0, n) holds
+// the position.
+constexpr int ATT_SRB = 4;
+template <int HD>
+__global__ __launch_bounds__(512) void k_attn_scores_rb(AttnArgs a, int m) {
+    constexpr int KS = HD + 1;
+    __shared__ float sk[ATT_CH * KS];
+    __shared__ __align__(16) float sq[ATT_SRB][ATT_MAX_GQA][HD];
+    const int gqa = a.n_head / a.n_kv_head;
+    const int lane = threadIdx.x & 63, hg = threadIdx.x >> 6;
+    const int kvh = blockIdx.x;
+    const size_t start = (size_t)blockIdx.y * ATT_CH;
+    const int i0 = blockIdx.z * ATT_SRB;
+    size_t t0[ATT_SRB], tn[ATT_SRB];
+    size_t lo = ~(size_t)0, hi = 0;
+#pragma unroll
+    for (int r = 0; r < ATT_SRB; r++) {
+        row_range(a, (size_t)min(i0 + r, m - 1), t0[r], tn[r]);
+        if (i0 + r >= m) tn[r] = t0[r];  // rows past m: empty
+        lo = min(lo, t0[r]);
+        hi = max(hi, tn[r]);
+    }
+    if (start >= hi || start + ATT_CH <= lo) return;  // no row has a position here
+    const size_t end = min(start + ATT_CH, hi);
+    const int rows = (int)(end - start);
+    const size_t kv = (size_t)a.n_kv_head * HD, q_dim = (size_t)a.n_head * HD;
+    const int nthreads = gqa * 64;
+    for (int e = threadIdx.x; e < ATT_SRB * gqa * HD; e += nthreads) {
+        const int r = e / (gqa * HD), hh = (e / HD) % gqa, d = e % HD;
+        const size_t i = (size_t)min(i0 + r, m - 1);
+        sq[r][hh][d] = a.q[i * q_dim + (size_t)(kvh * gqa + hh) * HD + d];
+    }
+    const float *kb = a.k_cache + start * kv + (size_t)kvh * HD;
+    constexpr int R4 = HD / 4;
+    for (int idx = threadIdx.x; idx < rows * R4; idx += nthreads) {
+        const int r = idx / R4, c4 = idx % R4;
+        const float4 k4 = *(const float4 *)(kb + (size_t)r * kv + 4 * c4);
+        float *d = sk + r * KS + 4 * c4;
+        d[0] = k4.x;
+        d[1] = k4.y;
+        d[2] = k4.z;
+        d[3] = k4.w;
+    }
+    __syncthreads();
+    if (lane >= rows) return;
+    const size_t t = start + lane;
+    const float *kr = sk + lane * KS;
+    float sc[ATT_SRB];
+#pragma unroll
+    for (int r = 0; r < ATT_SRB; r++) sc[r] = 0.0f;
+#pragma unroll 8
+    for (int d = 0; d < HD; d++) {
+        const float kd = kr[d];
+#pragma unroll
+        for (int r = 0; r < ATT_SRB; r++) sc[r] += sq[r][hg][d] * kd;
+    }
+#pragma unroll
+    for (int r = 0; r < ATT_SRB; r++)
+        if (t >= t0[r] && t < tn[r])
+            a.prob[((size_t)(i0 + r) * a.n_head + (size_t)(kvh * gqa + hg)) * a.span + (t - t0[r])] = sc[r] * a.scale;
+}
+
 // One wave's share of the q/k/v epilogue for one head vector (decode):
 // bias, rmsnorm_heads (sequential sum of squares by lane 0), rope with the
 // position's table row; the result is left in `hv` (LDS, hd floats).
@@ -848,10 +914,19 @@ void launch_attention(float *out, const float *q, const float *k_cache, const fl
     size_t span = window > 0 && window < ctx_rows ? window : ctx_rows;
     dim3 grid((unsigned)n_kv_head, (unsigned)((span + ATT_CH - 1) / ATT_CH), (unsigned)m);
     const unsigned threads = (unsigned)(64 * (n_head / n_kv_head));
-    switch (head_dim) {
-    case 64: k_attn_scores<64><<<grid, threads, 0, s>>>(a); break;
-    case 128: k_attn_scores<128><<<grid, threads, 0, s>>>(a); break;
-    default: k_attn_scores<256><<<grid, threads, 0, s>>>(a); break;
+    static const bool rb_off = getenv("AOTK_NO_SCORES_RB") != nullptr;
+    if (m > 1 && !pos_dev && !rb_off && head_dim <= 128) {
+        // several rows per block over absolute position chunks
+        const size_t hi = pos0 + m;  // the last row's end
+        dim3 g((unsigned)n_kv_head, (unsigned)((hi + ATT_CH - 1) / ATT_CH), (unsigned)((m + ATT_SRB - 1) / ATT_SRB));
+        if (head_dim == 64) k_attn_scores_rb<64><<<g, threads, 0, s>>>(a, (int)m);
+        else k_attn_scores_rb<128><<<g, threads, 0, s>>>(a, (int)m);
+    } else {
+        switch (head_dim) {
+        case 64: k_attn_scores<64><<<grid, threads, 0, s>>>(a); break;
+        case 128: k_attn_scores<128><<<grid, threads, 0, s>>>(a); break;
+        default: k_attn_scores<256><<<grid, threads, 0, s>>>(a); break;
+        }
     }
     // the longest row spans min(pos0 + m, window) positions
     const size_t longest = window > 0 && window < pos0 + m ? window : pos0 + m;

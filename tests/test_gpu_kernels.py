@@ -159,7 +159,7 @@ def _or_rmsnorm(oracle, x, w):
     return out
 
 
-@pytest.mark.parametrize("hd,nh,nkv,window", [(64, 32, 4, 0), (128, 32, 8, 0), (256, 8, 4, 5), (128, 4, 4, 0)])
+@pytest.mark.parametrize("hd,nh,nkv,window", [(64, 32, 4, 0), (128, 32, 8, 0), (256, 8, 4, 5), (128, 4, 4, 0), (64, 8, 2, 7), (128, 8, 8, 90)])
 def test_attention(aotk, oracle, hd, nh, nkv, window):
     rng = np.random.default_rng(hd + nh)
     ctx, layer = 150, 1
