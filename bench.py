@@ -32,6 +32,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [ROOT, os.path.join(ROOT, "aot-llm_amd")]
 
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 SEED = 0x5EED
 
 
@@ -214,6 +215,11 @@ def main():
     t_gen = time.perf_counter() - t
     tok_s = a.steps / t_gen
     wbytes = model.weight_bytes()
+    # int8 MFMA work of the prompt: 2 * tokens * the layer matrices' weights
+    # (the logits of a chunk come from its last row alone, a matvec)
+    layer_params = sum(getattr(L, n).rows * getattr(L, n).cols for L in spec.layers
+                       for n in ("wq", "wk", "wv", "wo", "gate", "up", "down"))
+    prompt_tops = 2.0 * layer_params * prompt_tok_s / 1e12
     log(f"decode: {a.steps} forwards in {t_gen * 1e3:.1f} ms ({tok_s:.1f} tok/s, "
         f"{wbytes * tok_s / 1e9:.0f} GB/s of weights)")
 
@@ -273,6 +279,8 @@ def main():
                                f"then greedy decode (batch 1)",
                    "prompt_tokens": a.prompt, "chunk": a.chunk, "seed": SEED},
         "prompt_tok_s": round(prompt_tok_s, 2),
+        "prompt_int8_TOPs": round(prompt_tops, 1),
+        "prompt_int8_frac": round(prompt_tops / INT8_PEAK_TOPS, 4),
         "decode_weight_bytes_per_token": wbytes,
         "decode_weight_GBs": round(wbytes * tok_s / 1e9, 1),
         "q4k_matvec": micro,
