@@ -10,6 +10,10 @@ weights and KV cache resident in HBM.
 
 Also reported on the same JSON line:
   prompt_tok_s   evaluated prompt tokens / prompt seconds (app.rs:651)
+  prompt_int8_TOPs / prompt_int8_frac
+                 the prompt's matmul work (2 x tokens x layer weights, 0.893
+                 TOP per 64-token chunk) per second, and against the MI355X
+                 dense int8 MFMA peak (5 POP/s)
   q4k_matvec     the Q4_K matvec kernel alone at the microbench shapes
                  (configs[1]), GB/s of algorithmic bytes, copies rotated past
                  the 256 MB Infinity Cache
