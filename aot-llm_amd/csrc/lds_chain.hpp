@@ -44,7 +44,7 @@ namespace aotk {
     "s_waitcnt lgkmcnt(" #W2 ")\n" LC_ADD4(120, 121, 122, 123)    \
     "s_waitcnt lgkmcnt(" #W3 ")\n" LC_ADD4(124, 125, 126, 127)
 // prologue: nothing else outstanding on the counter (it also counts scalar
-// loads, which would upset the waits below), then round 0 into set A
+// loads, which would upset the waits below), then the first round into set A
 #define LC_PRO "s_waitcnt lgkmcnt(0)\n" LC_RD(96, 0) LC_RD(100, 16) LC_RD(104, 32) LC_RD(108, 48)
 // a round: the next round (64 bytes on) into the other set, the adds of this
 // one, then the address moves on

@@ -80,7 +80,7 @@ def time_kernel(aotk, kind, rows, cols, iters=200, min_bytes=1 << 30):
 
 
 def extra_config(aotk, configs, name, n_ctx, steps):
-    """Decode tok/s of another BASELINE config at its context: the KV cache
+    """Decode tok/s of another benchmark config at its context: the KV cache
     holds n_ctx positions (random values uploaded, standing in for the
     prefill), then `steps` greedy forwards are timed."""
     import numpy as np

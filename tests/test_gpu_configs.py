@@ -1,4 +1,4 @@
-"""The BASELINE model shapes on the GPU against the oracle, bit for bit:
+"""The benchmark model shapes on the GPU against the oracle, bit for bit:
 greedy streams after a short prompt (batched prompt path) for the Llama-3-8B,
 Qwen3-8B and Gemma-3-4B configs, and single decode steps at the long
 contexts of the Qwen3 (4096 positions) and Gemma-3 (8192 positions, sliding
