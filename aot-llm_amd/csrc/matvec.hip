@@ -1123,7 +1123,7 @@ __global__ __launch_bounds__(256) void k_mv_q80(MvArgs a) {
 // step's weights are loaded during phase B. Then the avx2 horizontal sum.
 constexpr int Q8B_R = 4;
 constexpr int Q8B_MAX_COLS = 16384;
-constexpr int Q8B_PS = 64 * 9 + 8;  // floats per row in the P buffer (block stride 9, row pad 8)
+constexpr int Q8B_CS = 64 + 4;  // floats per (row, chain) line of the P buffer: chain-major, padded
 
 template <int KIND>
 struct Q8bW {
@@ -1139,8 +1139,8 @@ __global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
     // launch so that short rows leave LDS for more blocks per CU
     extern __shared__ __align__(16) int8_t sy[];
     float *syd = (float *)(sy + a.cols);
-    __shared__ float sP[4][R * Q8B_PS];
-    __shared__ float sD[4][R][64];
+    __shared__ __align__(16) float sP[4][R][8][Q8B_CS];
+    __shared__ __align__(16) float sD[4][R][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tok = blockIdx.y;
     const int nb = a.nb;
@@ -1230,9 +1230,8 @@ __global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
                         P[l] = (float)dot4(v, yw[l], off[l]);
                     }
                 }
-                float *dst = &sP[wave][r * Q8B_PS + lane * 9];
 #pragma unroll
-                for (int l = 0; l < 8; l++) dst[l] = P[l];
+                for (int l = 0; l < 8; l++) sP[wave][r][l][lane] = P[l];
                 sD[wave][r][lane] = f16_to_f32(w[r].d) * yd;
             }
         }
@@ -1240,20 +1239,24 @@ __global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
         // phase B: block order, one fma chain per (row, lane chain)
         if (rr < R) {
             const int n = nb - c0 < 64 ? nb - c0 : 64;
-            const float *pp = &sP[wave][rr * Q8B_PS + chain];
+            // chain-major P and contiguous D: 16-byte reads (D is the same
+            // for the row's 8 chains, a broadcast)
+            const float *pp = sP[wave][rr][chain];
             const float *dp = sD[wave][rr];
             int i = 0;
             for (; i + 8 <= n; i += 8) {
-                float pv[8], dv[8];
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    pv[k] = pp[(i + k) * 9];
-                    dv[k] = dp[i + k];
-                }
-#pragma unroll
-                for (int k = 0; k < 8; k++) acc = fmaf(dv[k], pv[k], acc);
+                const float4 p0 = *(const float4 *)(pp + i), p1 = *(const float4 *)(pp + i + 4);
+                const float4 d0 = *(const float4 *)(dp + i), d1 = *(const float4 *)(dp + i + 4);
+                acc = fmaf(d0.x, p0.x, acc);
+                acc = fmaf(d0.y, p0.y, acc);
+                acc = fmaf(d0.z, p0.z, acc);
+                acc = fmaf(d0.w, p0.w, acc);
+                acc = fmaf(d1.x, p1.x, acc);
+                acc = fmaf(d1.y, p1.y, acc);
+                acc = fmaf(d1.z, p1.z, acc);
+                acc = fmaf(d1.w, p1.w, acc);
             }
-            for (; i < n; i++) acc = fmaf(dp[i], pp[i * 9], acc);
+            for (; i < n; i++) acc = fmaf(dp[i], pp[i], acc);
         }
         wave_lds_sync();
     };
