@@ -31,6 +31,8 @@ def test_config_prompt_and_greedy(aotk, oracle, name):
     a, b = st.logits(), ref.logits()
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{name}: prompt logits differ"
     assert st.generate(n_prompt, n_gen) == ref.generate(n_prompt, n_gen)
+    # the last decode step's logits, bit for bit
+    assert np.array_equal(st.logits().view(np.uint32), ref.logits().view(np.uint32)), f"{name}: decode logits differ"
     ref.close()
     st.free()
     gm.free()
