@@ -140,17 +140,18 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant(const float *__restrict
     const float *xr = x + m * n;
     const int C = seq_chunk(n);
     RMS_TS(0);
-    // the norm weights are loaded before the sum (n <= 8 * blockDim.x)
-    float wv[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const int i = threadIdx.x + k * SEQ_T;
-        wv[k] = i < n ? w[i] : 0.0f;
-    }
-    // all of a thread's loads are in flight together (n <= 8 * blockDim.x)
-    float xv[8];
+    // all of a thread's loads are in flight together (n <= 8 * blockDim.x):
+    // the row first, then the norm weights, which stay in flight during the
+    // sum (the loads complete in order, so the squares wait for the row only)
+    float xv[8], wv[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) xv[k] = xr[min((int)threadIdx.x + k * SEQ_T, n - 1)];
+#pragma unroll
+    for (int k = 0; k < 8; k++) wv[k] = w[min((int)threadIdx.x + k * SEQ_T, n - 1)];
+    // the row is needed here, on every path: no load may move into the
+    // conditional stores below (and wait there for the norm weights)
+#pragma unroll
+    for (int k = 0; k < 8; k++) asm volatile("" : "+v"(xv[k]));
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         const int i = threadIdx.x + k * SEQ_T;
@@ -970,15 +971,19 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_add(float *x, const float *y,
     const float *yr = y + m * n;
     float *xr = x + m * n;
     const int C = seq_chunk(n);
-    // every load (y, and x and w for the update) is issued before the sum
+    // every load (y, and x and w for the update) is issued before the sum, y
+    // first: the loads complete in order, so the squares wait for y only
     float yv[8], xv[8], wv[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const int i = min((int)threadIdx.x + k * SEQ_T, n - 1);
-        yv[k] = yr[i];
-        xv[k] = xr[i];
-        wv[k] = w[i];
-    }
+    for (int k = 0; k < 8; k++) yv[k] = yr[min((int)threadIdx.x + k * SEQ_T, n - 1)];
+#pragma unroll
+    for (int k = 0; k < 8; k++) xv[k] = xr[min((int)threadIdx.x + k * SEQ_T, n - 1)];
+#pragma unroll
+    for (int k = 0; k < 8; k++) wv[k] = w[min((int)threadIdx.x + k * SEQ_T, n - 1)];
+    // y is needed here, on every path: no load may move into the conditional
+    // stores below (and wait there for x and w)
+#pragma unroll
+    for (int k = 0; k < 8; k++) asm volatile("" : "+v"(yv[k]));
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         const int i = threadIdx.x + k * SEQ_T;
