@@ -174,7 +174,9 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant(const float *__restrict
             if (out.f32) out.f32[m * n + i] = v;
         }
     }
+    RMS_TS(4);
     __syncthreads();
+    RMS_TS(5);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     ActQ8K qk = q8k_row(out.q8k, m, n);
     ActQ8_0 q0 = q80_row(out.q80, m, n);
