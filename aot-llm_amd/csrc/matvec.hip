@@ -412,6 +412,7 @@ __device__ __forceinline__ float kq_term(const uint4 (&c)[kq_chl<KIND, SPL>()], 
 // instantiation up to 32 super-blocks, else one.
 __host__ __device__ constexpr int kq_spl(int nb) { return nb > 0 && nb <= 32 ? 2 : 1; }
 
+// PF = 0: one row group per wave (G == 1), no second register set;
 // PF = 1: G groups per wave with the next group's loads in flight while the
 // current one computes; PF = 2: the same for G >= 2, with the second group's
 // loads issued together with the first's.
@@ -573,11 +574,12 @@ __global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq(MvArgs a, int RL, int
 // Two K-quant matrices of different kinds sharing the input in one launch
 // (q/k in one kind and v in another): blocks [0, nblk_a) run `a`, the rest
 // run `b`.
-template <int KA, int KB, int NB>
-__global__ __launch_bounds__(256, 2) void k_mv_kq2(MvArgs a, int RLa, int Ga, MvArgs b, int RLb, int Gb, int nblk_a) {
+// PF as for mv_kq_body (PF == 0 only with Ga == Gb == 1).
+template <int KA, int KB, int NB, int PF>
+__global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq2(MvArgs a, int RLa, int Ga, MvArgs b, int RLb, int Gb, int nblk_a) {
     __shared__ KqShared sh;
-    if ((int)blockIdx.x < nblk_a) mv_kq_body<KA, 1, NB>(a, RLa, Ga, blockIdx.x, sh.y, sh.t);
-    else mv_kq_body<KB, 1, NB>(b, RLb, Gb, blockIdx.x - nblk_a, sh.y, sh.t);
+    if ((int)blockIdx.x < nblk_a) mv_kq_body<KA, PF, NB>(a, RLa, Ga, blockIdx.x, sh.y, sh.t);
+    else mv_kq_body<KB, PF, NB>(b, RLb, Gb, blockIdx.x - nblk_a, sh.y, sh.t);
 }
 
 // The row lengths of the configs (cols / 256) get their own instantiations.
@@ -1536,12 +1538,24 @@ static void launch_kq(const MvArgs &a, dim3 grid, hipStream_t s) {
         int RL, G, blocks;
         kq_shape(a, RL, G, blocks);
         grid.x = (unsigned)blocks;
-        if (a.xq_src) {
+        // one group per wave: no next-group registers (more waves resident),
+        // except for Q6_K rows of one lane per super-block, measured faster
+        // with the loads of a second register set in flight
+        const bool pf0 = G == 1 && !(KIND == AOTK_Q6_K && kq_spl(a.nb) == 1);
+        if (a.xq_src && pf0) {
+#define F(NB) k_mv_kq<KIND, 0, NB, true><<<grid, 256, 0, s>>>(a, RL, G)
+            AOTK_NB_SWITCH(a.nb, F)
+#undef F
+        } else if (a.xq_src) {
 #define F(NB) k_mv_kq<KIND, 1, NB, true><<<grid, 256, 0, s>>>(a, RL, G)
             AOTK_NB_SWITCH(a.nb, F)
 #undef F
         } else if (G >= 2) {
 #define F(NB) k_mv_kq<KIND, 2, NB><<<grid, 256, 0, s>>>(a, RL, G)
+            AOTK_NB_SWITCH(a.nb, F)
+#undef F
+        } else if (pf0) {
+#define F(NB) k_mv_kq<KIND, 0, NB><<<grid, 256, 0, s>>>(a, RL, G)
             AOTK_NB_SWITCH(a.nb, F)
 #undef F
         } else {
@@ -1726,12 +1740,21 @@ void launch_matvec_pair(int na, const DevWeight *const wa[], float *const ya[], 
     kq_shape(a, RLa, Ga, na_blk);
     kq_shape(b, RLb, Gb, nb_blk);
     dim3 grid((unsigned)(na_blk + nb_blk), (unsigned)m);
-    if (wa[0]->kind == AOTK_Q4_K) {
-#define F(NB) k_mv_kq2<AOTK_Q4_K, AOTK_Q6_K, NB><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk)
+    const bool q4 = wa[0]->kind == AOTK_Q4_K;
+    if (Ga == 1 && Gb == 1 && q4) {
+#define F(NB) k_mv_kq2<AOTK_Q4_K, AOTK_Q6_K, NB, 0><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk)
+        AOTK_NB_SWITCH(a.nb, F)
+#undef F
+    } else if (Ga == 1 && Gb == 1) {
+#define F(NB) k_mv_kq2<AOTK_Q5_K, AOTK_Q6_K, NB, 0><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk)
+        AOTK_NB_SWITCH(a.nb, F)
+#undef F
+    } else if (q4) {
+#define F(NB) k_mv_kq2<AOTK_Q4_K, AOTK_Q6_K, NB, 1><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk)
         AOTK_NB_SWITCH(a.nb, F)
 #undef F
     } else {
-#define F(NB) k_mv_kq2<AOTK_Q5_K, AOTK_Q6_K, NB><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk)
+#define F(NB) k_mv_kq2<AOTK_Q5_K, AOTK_Q6_K, NB, 1><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk)
         AOTK_NB_SWITCH(a.nb, F)
 #undef F
     }
