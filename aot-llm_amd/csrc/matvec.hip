@@ -1511,11 +1511,12 @@ static MvArgs make_args(int n, const DevWeight *const ws[], float *const ys[], c
 }
 
 // Row slots per wave (RL), row groups per wave (G) and blocks of the
-// K-quant kernel. One row group per wave up to 16384 groups of the unsplit
+// K-quant kernel. One row group per wave up to 65536 groups of the unsplit
 // size (several rounds of resident waves: measured faster than fewer waves
 // each running G groups with the next group's loads in flight, e.g. Q4_K
-// 14336x4096 7.8 against 8.8 us with three waves per SIMD in one round);
-// larger launches (lm-head) give each wave G groups.
+// 14336x4096 7.8 against 8.8 us with three waves per SIMD in one round,
+// the 128256x4096 lm-head 48.4 against 49.9 us with two groups per wave);
+// larger launches give each wave G groups.
 static bool nb_specialized(int nb) {
     return nb == 8 || nb == 10 || nb == 16 || nb == 22 || nb == 40 || nb == 48 || nb == 56;
 }
@@ -1524,9 +1525,9 @@ static void kq_shape(const MvArgs &a, int &RL, int &G, int &blocks) {
     // rows per group: every lane slot of spl * nb lanes that fits
     RL = 64 / (kq_spl(nb_specialized(a.nb) ? a.nb : 0) * a.nb);
     const int groups = (a.total_rows + RL - 1) / RL;
-    // groups per wave: one while the launch has at most 16384 groups of the
+    // groups per wave: one while the launch has at most 65536 groups of the
     // unsplit size (groups of the two-lane split hold half as many rows)
-    const int gcap = 16384 * (64 / a.nb) / RL;
+    const int gcap = 65536 * (64 / a.nb) / RL;
     G = (groups + gcap - 1) / gcap;
     G = G > 8 ? 8 : G;
     blocks = (groups + 4 * G - 1) / (4 * G);
