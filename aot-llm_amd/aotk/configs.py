@@ -31,6 +31,9 @@ ARCH_FLAGS = {
     "qwen2": dict(rope_neox=1, qkv_bias=1),
     "qwen3": dict(rope_neox=1, qk_norm=1),
     "gemma3": dict(rope_neox=1, qk_norm=1, embd_scale=1, post_norms=1, gelu=1, swa_pattern=6),
+    # Phi-3: NEOX RoPE; its fused attn_qkv / ffn_up are row views of one
+    # tensor (model.rs:257-262), the same arithmetic as separate tensors.
+    "phi3": dict(rope_neox=1),
 }
 
 CONFIGS = {
@@ -59,6 +62,8 @@ E2E_KINDS = [
     (abi.Q4_K, abi.Q4_0, abi.Q8_0, abi.Q5_K, abi.Q4_K, abi.Q4_K, abi.Q6_K),
     (abi.F16, abi.BF16, abi.F32, abi.Q4_0, abi.Q8_0, abi.Q8_0, abi.Q5_0),
 ]
+# Fused tensors share one format across their parts (tests/e2e.rs:416-421).
+E2E_FUSED_KINDS = [tuple(k[i] for i in (0, 0, 0, 3, 4, 4, 6)) for k in E2E_KINDS]
 TINY = dict(dim=256, hidden=512, n_head=4, n_kv_head=2, head_dim=64, vocab=512, eps=1e-5,
             rope_base=10000.0, n_ctx_train=512)
 TEST_CONFIGS = {
@@ -67,6 +72,7 @@ TEST_CONFIGS = {
     "tiny-qwen3": dict(TINY, arch="qwen3", n_layer=2, head_dim=128, mix="e2e"),
     "tiny-gemma3": dict(TINY, arch="gemma3", n_layer=6, mix="e2e", swa_window=4, rope_base=1000000.0,
                         rope_scale=2.0, tied=False),
+    "tiny-phi3": dict(TINY, arch="phi3", n_layer=2, mix="e2e-fused"),
     "tiny-q4km": dict(TINY, arch="llama", n_layer=2, mix="q4_k_m"),
     "tiny-q8_0": dict(TINY, arch="qwen3", n_layer=2, head_dim=128, mix="q8_0"),
     "tiny-q5km": dict(TINY, arch="gemma3", n_layer=6, mix="q5_k_m", swa_window=4, tied=True),
@@ -97,14 +103,14 @@ class Spec:
         mix = cfg["mix"]
 
         def kind_of(slot, layer):
-            if mix == "e2e":
-                ks = E2E_KINDS[layer % 2]
+            if mix in ("e2e", "e2e-fused"):
+                ks = (E2E_KINDS if mix == "e2e" else E2E_FUSED_KINDS)[layer % 2]
                 idx = ("wq", "wk", "wv", "wo", "gate", "up", "down").index(slot)
                 return ks[idx]
             return MIXES[mix][slot]
 
-        embd_kind = abi.Q4_K if mix == "e2e" else MIXES[mix]["embd"]
-        out_kind = abi.Q6_K if mix == "e2e" else MIXES[mix]["output"]
+        embd_kind = abi.Q4_K if mix.startswith("e2e") else MIXES[mix]["embd"]
+        out_kind = abi.Q6_K if mix.startswith("e2e") else MIXES[mix]["output"]
         self.spec = abi.ModelSpec()
         s = self.spec
         for k, v in d.items():

@@ -414,8 +414,9 @@ __host__ __device__ constexpr int kq_spl(int nb) { return nb > 0 && nb <= 32 ? 2
 
 // PF = 0: one row group per wave (G == 1), no second register set;
 // PF = 1: G groups per wave with the next group's loads in flight while the
-// current one computes; PF = 2: the same for G >= 2, with the second group's
-// loads issued together with the first's.
+// current one computes (launched with G == 1 for Q6_K rows of one lane per
+// super-block and for the f32-input variant, whose register budget of two
+// waves per SIMD measured faster there).
 // NB > 0: the super-blocks per row as a compile-time constant (immediate
 // chunk offsets, constant row-slot division, an unmasked fold); NB == 0 reads
 // it from the arguments.
@@ -456,9 +457,8 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
     MV_TS(0);
     // This token's Q8_K activation is loaded first (<= 64 super-blocks: four
     // quads of qs, one of bsums and one scale per thread; indices past the
-    // end repeat the last element), then the weights of the first group (and
-    // with PF == 2 of the second): waiting for the activation then leaves
-    // the weights in flight.
+    // end repeat the last element), then the weights of the first group:
+    // waiting for the activation then leaves the weights in flight.
     constexpr bool stage = !QSRC;  // QSRC: the input arrives in f32 (a.xq_src) and is quantized here
     const int nq = nb * 16;
     uint4 xv[4], bv;
@@ -476,7 +476,6 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
         for (int k = 0; k < 4; k++) xf[k] = ((const float4 *)(a.xq_src + (size_t)min(wave + 4 * k, nb - 1) * 256))[lane];
     }
     load(cur, dcur, 0);
-    if (PF == 2) load(nxt, dnxt, 1);  // G >= 2
     if constexpr (stage) {
         // unconditional stores: past the end they repeat the last element
 #pragma unroll
@@ -551,7 +550,7 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
     // groups alternate between the two register buffers (no copies)
     for (int gi = 0; gi < ng; gi += 2) {
         if ((group0 + gi) * RL >= a.total_rows) break;
-        if (PF && gi + 1 < ng && !(PF == 2 && gi == 0)) load(nxt, dnxt, gi + 1);
+        if (PF && gi + 1 < ng) load(nxt, dnxt, gi + 1);
         group(cur, dcur, gi);
         if (!PF || gi + 1 >= ng || (group0 + gi + 1) * RL >= a.total_rows) break;
         if (gi + 2 < ng) load(cur, dcur, gi + 2);
@@ -574,7 +573,7 @@ __global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq(MvArgs a, int RL, int
 // Two K-quant matrices of different kinds sharing the input in one launch
 // (q/k in one kind and v in another): blocks [0, nblk_a) run `a`, the rest
 // run `b`.
-// PF as for mv_kq_body (PF == 0 only with Ga == Gb == 1).
+// PF as for mv_kq_body (launched with PF == 0).
 template <int KA, int KB, int NB, int PF>
 __global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq2(MvArgs a, int RLa, int Ga, MvArgs b, int RLb, int Gb, int nblk_a) {
     __shared__ KqShared sh;
@@ -1511,12 +1510,11 @@ static MvArgs make_args(int n, const DevWeight *const ws[], float *const ys[], c
 }
 
 // Row slots per wave (RL), row groups per wave (G) and blocks of the
-// K-quant kernel. One row group per wave up to 65536 groups of the unsplit
-// size (several rounds of resident waves: measured faster than fewer waves
-// each running G groups with the next group's loads in flight, e.g. Q4_K
-// 14336x4096 7.8 against 8.8 us with three waves per SIMD in one round,
-// the 128256x4096 lm-head 48.4 against 49.9 us with two groups per wave);
-// larger launches give each wave G groups.
+// K-quant kernel. One row group per wave at every size: several rounds of
+// resident waves measured faster than fewer waves each running G groups with
+// the next group's loads in flight (Q4_K 14336x4096 7.8 against 8.8 us with
+// three waves per SIMD in one round, the 128256x4096 lm-head 48.4 against
+// 49.9 us with two groups per wave).
 static bool nb_specialized(int nb) {
     return nb == 8 || nb == 10 || nb == 16 || nb == 22 || nb == 40 || nb == 48 || nb == 56;
 }
@@ -1525,12 +1523,8 @@ static void kq_shape(const MvArgs &a, int &RL, int &G, int &blocks) {
     // rows per group: every lane slot of spl * nb lanes that fits
     RL = 64 / (kq_spl(nb_specialized(a.nb) ? a.nb : 0) * a.nb);
     const int groups = (a.total_rows + RL - 1) / RL;
-    // groups per wave: one while the launch has at most 65536 groups of the
-    // unsplit size (groups of the two-lane split hold half as many rows)
-    const int gcap = 65536 * (64 / a.nb) / RL;
-    G = (groups + gcap - 1) / gcap;
-    G = G > 8 ? 8 : G;
-    blocks = (groups + 4 * G - 1) / (4 * G);
+    G = 1;
+    blocks = (groups + 3) / 4;
 }
 
 template <int KIND>
@@ -1551,10 +1545,6 @@ static void launch_kq(const MvArgs &a, dim3 grid, hipStream_t s) {
 #define F(NB) k_mv_kq<KIND, 1, NB, true><<<grid, 256, 0, s>>>(a, RL, G)
             AOTK_NB_SWITCH(a.nb, F)
 #undef F
-        } else if (G >= 2) {
-#define F(NB) k_mv_kq<KIND, 2, NB><<<grid, 256, 0, s>>>(a, RL, G)
-            AOTK_NB_SWITCH(a.nb, F)
-#undef F
         } else if (pf0) {
 #define F(NB) k_mv_kq<KIND, 0, NB><<<grid, 256, 0, s>>>(a, RL, G)
             AOTK_NB_SWITCH(a.nb, F)
@@ -1573,8 +1563,7 @@ static void launch_kq(const MvArgs &a, dim3 grid, hipStream_t s) {
 static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
     dim3 grid;
     grid.y = (unsigned)m;
-    if (m >= MM_MIN_TOKENS && m <= MM_TOK && (kind == AOTK_Q4_K || kind == AOTK_Q5_K || kind == AOTK_Q6_K) &&
-        !getenv("AOTK_NO_MFMA")) {
+    if (m >= MM_MIN_TOKENS && m <= MM_TOK && (kind == AOTK_Q4_K || kind == AOTK_Q5_K || kind == AOTK_Q6_K)) {
         // 64 rows per block; the token tiles per block are cut until the
         // grid reaches 512 blocks (small matrices) or one tile is left
         const unsigned rb = (unsigned)((a.total_rows + 63) / 64);
@@ -1588,8 +1577,7 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
         // down 82 -> 69 us, the 4096/5120-row Q4_K wo and q/k 20/24 -> 19/22
         // us, the 28672-row gate/up unchanged); fewer rows leave too few
         // blocks (the 1024-row v: 12 -> 21 us) and keep the kernels below
-        static const bool kt_off = getenv("AOTK_NO_MM_KT") != nullptr;
-        if (a.total_rows >= 2048 && !kt_off) {
+        if (a.total_rows >= 2048) {
             dim3 gk((unsigned)((a.total_rows + 15) / 16), 1);
             switch (kind) {
             case AOTK_Q4_K: k_mm_kt<AOTK_Q4_K><<<gk, 256, 0, s>>>(a, (int)m); break;
@@ -1666,7 +1654,7 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
     case AOTK_BF16: {
         grid.x = (unsigned)((a.total_rows + 31) / 32);
         const bool bf = kind == AOTK_BF16;
-        if (mv_half_fits(a) && !getenv("AOTK_NO_MVH")) {
+        if (mv_half_fits(a)) {
             const int n8 = (int)(a.cols >> 3);
             const size_t lds = 8 * sizeof(float) * (size_t)(((n8 + 31) & ~31) + 4);
             // deeper prefetch when few rows leave few waves in flight
@@ -1707,7 +1695,7 @@ void launch_matvec_multi(int n, const DevWeight *const ws[], float *const ys[], 
 
 bool launch_matvec_quant(const DevWeight &w, const float *x, float *y, const float *add, hipStream_t s) {
     const int kind = w.kind;
-    if ((kind != AOTK_Q4_K && kind != AOTK_Q5_K && kind != AOTK_Q6_K) || w.nb > 64 || getenv("AOTK_NO_MVQ"))
+    if ((kind != AOTK_Q4_K && kind != AOTK_Q5_K && kind != AOTK_Q6_K) || w.nb > 64)
         return false;
     const DevWeight *ws[1] = {&w};
     float *ys[1] = {y};
@@ -1741,21 +1729,12 @@ void launch_matvec_pair(int na, const DevWeight *const wa[], float *const ya[], 
     kq_shape(a, RLa, Ga, na_blk);
     kq_shape(b, RLb, Gb, nb_blk);
     dim3 grid((unsigned)(na_blk + nb_blk), (unsigned)m);
-    const bool q4 = wa[0]->kind == AOTK_Q4_K;
-    if (Ga == 1 && Gb == 1 && q4) {
+    if (wa[0]->kind == AOTK_Q4_K) {
 #define F(NB) k_mv_kq2<AOTK_Q4_K, AOTK_Q6_K, NB, 0><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk)
         AOTK_NB_SWITCH(a.nb, F)
 #undef F
-    } else if (Ga == 1 && Gb == 1) {
-#define F(NB) k_mv_kq2<AOTK_Q5_K, AOTK_Q6_K, NB, 0><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk)
-        AOTK_NB_SWITCH(a.nb, F)
-#undef F
-    } else if (q4) {
-#define F(NB) k_mv_kq2<AOTK_Q4_K, AOTK_Q6_K, NB, 1><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk)
-        AOTK_NB_SWITCH(a.nb, F)
-#undef F
     } else {
-#define F(NB) k_mv_kq2<AOTK_Q5_K, AOTK_Q6_K, NB, 1><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk)
+#define F(NB) k_mv_kq2<AOTK_Q5_K, AOTK_Q6_K, NB, 0><<<grid, 256, 0, s>>>(a, RLa, Ga, b, RLb, Gb, na_blk)
         AOTK_NB_SWITCH(a.nb, F)
 #undef F
     }

@@ -917,8 +917,7 @@ void launch_attention(float *out, const float *q, const float *k_cache, const fl
     size_t span = window > 0 && window < ctx_rows ? window : ctx_rows;
     dim3 grid((unsigned)n_kv_head, (unsigned)((span + ATT_CH - 1) / ATT_CH), (unsigned)m);
     const unsigned threads = (unsigned)(64 * (n_head / n_kv_head));
-    static const bool rb_off = getenv("AOTK_NO_SCORES_RB") != nullptr;
-    if (m > 1 && !pos_dev && !rb_off && head_dim <= 128) {
+    if (m > 1 && !pos_dev && head_dim <= 128) {
         // several rows per block over absolute position chunks
         const size_t hi = pos0 + m;  // the last row's end
         dim3 g((unsigned)n_kv_head, (unsigned)((hi + ATT_CH - 1) / ATT_CH), (unsigned)((m + ATT_SRB - 1) / ATT_SRB));
@@ -933,8 +932,7 @@ void launch_attention(float *out, const float *q, const float *k_cache, const fl
     }
     // the longest row spans min(pos0 + m, window) positions
     const size_t longest = window > 0 && window < pos0 + m ? window : pos0 + m;
-    static const bool rows_off = getenv("AOTK_NO_ATT_ROWS") != nullptr;  // the per-block path, for comparison
-    if (m > 1 && !pos_dev && longest <= (size_t)ATT_ROWS_MAX && !rows_off)
+    if (m > 1 && !pos_dev && longest <= (size_t)ATT_ROWS_MAX)
         launch_rows(a, head_dim, m, s);
     else
         launch_sv(a, head_dim, m, s);

@@ -47,6 +47,7 @@ static int fail(const char *fmt, ...) {
 
 static int g_device = -1;
 static hipStream_t g_stream = nullptr;
+static bool g_decode_graphs = true;  // set by aotk_init
 
 // Library scratch for the per-kernel entry points (grown on demand).
 static void *g_scratch = nullptr;
@@ -86,6 +87,10 @@ int aotk_init(int device) {
     HIPC(hipSetDevice(device));
     HIPC(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     g_device = device;
+    // the one run-time option: AOTK_NO_GRAPH=1 replays decode loops as plain
+    // stream launches (for kernel traces that list every launch)
+    const char *ng = getenv("AOTK_NO_GRAPH");
+    g_decode_graphs = !(ng && ng[0] && ng[0] != '0');
     return 0;
 }
 
@@ -1067,7 +1072,7 @@ int aotk_generate_greedy(aotk_state *st, size_t pos, size_t n, uint32_t *tokens_
         run_decode_step(st, 1);
         launch_inc((int *)(st->ctl + 1), g_stream);
     };
-    if (n > 1 && !st->gen_exec && !getenv("AOTK_NO_GRAPH")) {
+    if (n > 1 && !st->gen_exec && g_decode_graphs) {
         hipGraph_t graph = nullptr;
         HIPC(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal));
         step();
@@ -1232,7 +1237,7 @@ int aotk_generate(aotk_state *st, aotk_sampler *sp, size_t pos, size_t n, const 
     // the captured step bakes in the sampler's config and rng address
     const bool same = st->samp_exec && st->samp_rng == (const void *)sp->rng &&
                       memcmp(&st->samp_cfg, &sp->cfg, sizeof(sp->cfg)) == 0;
-    if (n > 1 && !same && !getenv("AOTK_NO_GRAPH")) {
+    if (n > 1 && !same && g_decode_graphs) {
         if (st->samp_exec) (void)hipGraphExecDestroy(st->samp_exec);
         st->samp_exec = nullptr;
         hipGraph_t graph = nullptr;

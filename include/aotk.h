@@ -118,7 +118,11 @@ typedef struct aotk_model_spec {
 /* Last error of the calling thread (capi.rs:129-141 `aot_last_error`). */
 const char *aotk_last_error(void);
 
-/* Select the device and create the library stream. Idempotent. */
+/* Select the device and create the library stream. Idempotent. Reads one
+ * environment option: AOTK_NO_GRAPH=1 runs the device-side generation loops
+ * (aotk_generate_greedy, aotk_generate) as plain stream launches instead of
+ * replaying a captured HIP graph per token, so kernel traces list every
+ * launch; results are identical either way. */
 int aotk_init(int device);
 
 /* Device memory helpers (so C/Rust/Python callers need no HIP headers). */

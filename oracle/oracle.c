@@ -1466,6 +1466,18 @@ float or_synth_value(uint64_t seed, uint32_t tensor_index, uint64_t elem) {
     return (float)s * SYNTH_SCALE;
 }
 
+void or_e2e_uniform(uint64_t *state, float a, float *out, size_t n) {
+    uint64_t s = *state;
+    for (size_t i = 0; i < n; i++) {
+        s ^= s << 13; /* e2e.rs:84-89 */
+        s ^= s >> 7;
+        s ^= s << 17;
+        float u = (float)(s % 1000001ULL) / 500000.0f - 1.0f; /* :91 */
+        out[i] = u * a;
+    }
+    *state = s;
+}
+
 typedef struct { const aotk_tensor *t; uint32_t idx; int is_norm; } synth_item;
 
 static int spec_items(const aotk_model_spec *spec, synth_item *items) {

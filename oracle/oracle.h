@@ -112,6 +112,11 @@ float or_synth_value(uint64_t seed, uint32_t tensor_index, uint64_t elem);
  * aotk_layer field order) 3 + 16*l + s. */
 int or_synth_blob(const aotk_model_spec *spec, uint64_t seed, uint8_t *blob, size_t blob_len, int n_threads);
 
+/* crates/aot-llm/tests/e2e.rs:81-95 `Rng`: xorshift64 (13, 7, 17) with
+ * uniform(a) = ((next % 1000001) as f32 / 500000 - 1) * a; fills out[0..n)
+ * in stream order and advances *state. */
+void or_e2e_uniform(uint64_t *state, float a, float *out, size_t n);
+
 /* Model runtime (state.rs, emit.rs forward/forward_batch) */
 typedef struct or_model or_model;
 or_model *or_model_new(const aotk_model_spec *spec, const uint8_t *blob, size_t blob_len,

@@ -65,6 +65,7 @@ def load():
     sig("or_argmax", u32, [vp, sz])
     sig("or_synth_value", f, [u64, u32, u64])
     sig("or_synth_blob", i, [vp, u64, vp, sz, i])
+    sig("or_e2e_uniform", None, [C.POINTER(u64), f, vp, sz])
     sig("or_model_new", vp, [vp, vp, sz, sz, sz, i, i])
     sig("or_model_free", None, [vp])
     sig("or_forward", i, [vp, u32, sz, i])

@@ -12,8 +12,9 @@ NAMES = dict(zip(ALL, ["f32", "f16", "bf16", "q4_0", "q5_0", "q8_0", "q4_K", "q5
 
 def cols_for(kind):
     return {F32: [8, 64, 2053, 4096], F16: [8, 64, 2053, 4096, 11008, 16384], BF16: [12, 64, 2053, 4096, 14336],
-            Q4_0: [32, 96, 2048, 5632], Q5_0: [32, 96, 2048], Q8_0: [32, 96, 2048, 12288],
-            Q4_K: [256, 512, 2048, 3072, 5632, 14336, 17408], Q5_K: [256, 512, 2560, 10240],
+            Q4_0: [32, 96, 2048, 4096, 5632, 14336, 16384, 18432], Q5_0: [32, 96, 2048, 4096, 14336, 16384, 18432],
+            Q8_0: [32, 96, 2048, 4096, 12288, 14336, 16384, 18432],
+            Q4_K: [256, 512, 2048, 3072, 5632, 14336, 17408], Q5_K: [256, 512, 2560, 4096, 10240, 14336],
             Q6_K: [256, 512, 2048, 5632, 14336, 17408]}[kind]
 
 
@@ -80,6 +81,31 @@ def test_matvec_bitexact(aotk, oracle, kind):
         assert np.array_equal(got2.view(np.uint32), ref.view(np.uint32))
 
 
+MICRO_KINDS = [Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, Q5_0, F16, BF16]
+MICRO_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (128256, 4096)]
+
+
+@pytest.mark.parametrize("kind", MICRO_KINDS, ids=lambda k: NAMES[k])
+def test_matvec_microbench_shapes(aotk, oracle, kind):
+    """Every cell of the configs[1] microbench (8 kinds x 4 shapes, the
+    lm-head included) bit-exact against the oracle. The rows are 509 distinct
+    encoded rows repeated (the kernels' row mapping and launch shape are those
+    of the full matrix; only the host encoding is shortened)."""
+    rng = np.random.default_rng(200 + kind)
+    pool = oracle.Pool(16)
+    for rows, cols in MICRO_SHAPES:
+        base = weights(kind, 509, cols, kind * 11 + cols, oracle)
+        raw = np.resize(base, (rows, base.shape[1]))
+        x = (rng.standard_normal(cols)).astype(np.float32)
+        act = oracle.quantize_act(kind, x)
+        ref = oracle.matvec(kind, raw, act, rows, cols, pool=pool)
+        w = aotk.Weight(kind, raw, rows, cols)
+        got = aotk.matvec(w, act)
+        w.free()
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), \
+            f"{NAMES[kind]} {rows}x{cols}: {int((got != ref).sum())} rows differ"
+
+
 @pytest.mark.parametrize("kind", [F16, BF16], ids=lambda k: NAMES[k])
 def test_matvec_half_many_rows(aotk, oracle, kind):
     """The shallow-prefetch variant for matrices of 16384 rows or more, and a
@@ -122,6 +148,26 @@ def test_matmul_many_rows(aotk, oracle, kind):
         got = aotk.matmul(w, acts, m)
         ref = oracle.matmul(kind, raw, acts, m, rows, cols).reshape(m, rows)
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), m
+
+
+@pytest.mark.parametrize("kind,rows,cols", [(Q4_K, 4096, 4096), (Q4_K, 1024, 4096), (Q6_K, 1024, 4096),
+                                            (Q4_K, 14336, 4096), (Q6_K, 4096, 14336)],
+                         ids=["wq", "wk", "wv", "gate", "down"])
+def test_matmul_llama3_layer_chunk(aotk, oracle, kind, rows, cols):
+    """One 64-token prompt chunk through every matrix shape of a Llama-3-8B
+    Q4_K_M layer, bit-exact: the 16-row whole-batch kernel at
+    4096+ rows and the split kernel at 1024 rows (509 distinct rows tiled)."""
+    rng = np.random.default_rng(rows + cols + kind)
+    m = 64
+    base = weights(kind, 509, cols, rows, oracle)
+    raw = np.resize(base, (rows, base.shape[1]))
+    w = aotk.Weight(kind, raw, rows, cols)
+    xs = [(rng.standard_normal(cols)).astype(np.float32) for _ in range(m)]
+    acts = np.concatenate([oracle.quantize_act(kind, x) for x in xs])
+    got = aotk.matmul(w, acts, m)
+    ref = oracle.matmul(kind, raw, acts, m, rows, cols, pool=oracle.Pool(16)).reshape(m, rows)
+    w.free()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
 def test_rope_bitexact(aotk, oracle):

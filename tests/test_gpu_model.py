@@ -81,3 +81,41 @@ def test_tinyllama_config_greedy_stream(aotk, oracle):
     assert rel_l2(st.logits(), ref.logits()) < 1e-3
     assert np.array_equal(st.logits(), ref.logits())
     assert st.generate(6, 32) == ref.generate(6, 32)
+
+
+E2E_CASES = ["tiny-llama", "tiny-qwen2", "tiny-qwen3", "tiny-phi3", "tiny-gemma3", "tiny-q4km", "tiny-q8_0", "tiny-q5km"]
+
+
+@pytest.mark.parametrize("name", E2E_CASES)
+def test_e2e_models_bitexact(aotk, oracle, name):
+    """The models tests/test_oracle_forward.py pins the oracle's forward with
+    (built like crates/aot-llm/tests/e2e.rs:406-437, larger weights than the
+    synthetic generator), token by token and batched, on the GPU: logits bit
+    for bit equal to the oracle's, and the same greedy continuation."""
+    from aotk import configs, gguf
+    from e2e_models import build_e2e_blob
+    spec = configs.build(name)
+    blob = build_e2e_blob(spec)
+    if name == "tiny-phi3":
+        b = gguf.config_gguf(spec, blob, "phi3", fuse=True)
+        f = gguf.GgufFile(b)
+        spec = gguf.GgufSpec(f)
+        blob = np.frombuffer(b, np.uint8)[f.data_offset:f.data_offset + f.data_len()].copy()
+    n = 13 if spec.spec.dims.swa_window else 7
+    toks = configs.prompt_tokens(0xE2E, n, spec.d["vocab"])
+    ctx = n + 10
+    gm = aotk.Model(spec, blob)
+    for batch in (1, 64):
+        ref = oracle.Model(spec, blob, ctx)
+        st = aotk.State(gm, ctx)
+        if batch == 1:
+            for i, t in enumerate(toks):
+                ref.forward(t, i, i + 1 == n)
+                st.forward(t, i, i + 1 == n)
+        else:
+            ref.prompt(toks, batch=batch)
+            st.prompt(toks, batch=batch)
+        a, b = st.logits(), ref.logits()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"batch {batch}: rel L2 {rel_l2(a, b):.3g}"
+        assert st.generate(n, 8) == ref.generate(n, 8)
+        ref.close()
