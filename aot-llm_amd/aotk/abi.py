@@ -128,6 +128,7 @@ def load(path=None):
     _sig(lib, "aotk_matvec", i, [vp, vp, vp])
     _sig(lib, "aotk_matvec_f32", i, [vp, vp, vp])
     _sig(lib, "aotk_matmul", i, [vp, vp, sz, vp])
+    _sig(lib, "aotk_matmul_noalloc", i, [vp, vp, sz, vp])
     _sig(lib, "aotk_rmsnorm", i, [vp, vp, vp, sz, sz, C.c_float])
     _sig(lib, "aotk_rmsnorm_heads", i, [vp, vp, sz, sz, C.c_float])
     _sig(lib, "aotk_rope", i, [vp, sz, sz, sz, sz, vp, i])

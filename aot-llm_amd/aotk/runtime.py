@@ -154,6 +154,16 @@ def matmul(w, xs_act, m):
     return out.to_numpy(np.float32).reshape(m, w.rows)
 
 
+def matmul_noalloc(w, xs_act, m):
+    """aotk_matmul_noalloc: the same product staged in the library's fixed
+    device array (the caller's buffers are allocated here, the call itself
+    allocates nothing)."""
+    dx = DeviceBuffer.from_numpy(np.ascontiguousarray(xs_act))
+    out = DeviceBuffer(m * w.rows * 4)
+    abi.check(_lib().aotk_matmul_noalloc(w.h, dx.ptr, m, out.ptr))
+    return out.to_numpy(np.float32).reshape(m, w.rows)
+
+
 def matvec_f32(w, x):
     dx = DeviceBuffer.from_numpy(np.ascontiguousarray(x, np.float32))
     out = DeviceBuffer(w.rows * 4)

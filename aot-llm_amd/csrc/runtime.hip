@@ -53,12 +53,21 @@ static bool g_decode_graphs = true;  // set by aotk_init
 static void *g_scratch = nullptr;
 static size_t g_scratch_bytes = 0;
 
+// Staging memory of aotk_matmul_noalloc: a fixed device array (one copy per
+// GPU, held until the process ends) instead of the growable scratch above.
+// Host code never passes `scratch` itself (its host-side name is not a
+// device address): aotk_init looks its address up per device.
+static constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(4) << 20;
+static constexpr int NOALLOC_MAX_DEVICES = 64;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+static void *g_noalloc_scratch[NOALLOC_MAX_DEVICES] = {};
+
 static int ensure_init() {
     if (g_stream) return 0;
     return aotk_init(0);
 }
 
-static void *scratch(size_t bytes) {
+static void *lib_scratch(size_t bytes) {
     if (bytes <= g_scratch_bytes) return g_scratch;
     if (g_scratch) (void)hipFree(g_scratch);
     g_scratch = nullptr;
@@ -91,6 +100,10 @@ int aotk_init(int device) {
     // stream launches (for kernel traces that list every launch)
     const char *ng = getenv("AOTK_NO_GRAPH");
     g_decode_graphs = !(ng && ng[0] && ng[0] != '0');
+    if (device >= NOALLOC_MAX_DEVICES) return fail("aotk_init: device %d beyond the supported %d", device, NOALLOC_MAX_DEVICES);
+    void *na = nullptr;
+    HIPC(hipGetSymbolAddress(&na, HIP_SYMBOL(scratch)));
+    g_noalloc_scratch[device] = na;
     return 0;
 }
 
@@ -231,7 +244,7 @@ int aotk_quantize_rows(int kind, const float *x_dev, size_t rows, size_t cols, v
 int aotk_quantize_q8_0(const float *x_dev, size_t n, aotk_block_q8_0 *out_dev) {
     if (ensure_init()) return -1;
     if (n % 32) return fail("quantize_q8_0: n = %zu is not a multiple of 32", n);
-    void *s = scratch(act_q8_0_bytes(n, 1));
+    void *s = lib_scratch(act_q8_0_bytes(n, 1));
     if (!s) return -1;
     ActQ8_0 a = act_q8_0_view(s, n, 1);
     launch_quant_q8_0(x_dev, n, 1, a, g_stream);
@@ -244,7 +257,7 @@ int aotk_quantize_q8_0(const float *x_dev, size_t n, aotk_block_q8_0 *out_dev) {
 int aotk_quantize_q8_k(const float *x_dev, size_t n, aotk_block_q8_k *out_dev) {
     if (ensure_init()) return -1;
     if (n % 256) return fail("quantize_q8_k: n = %zu is not a multiple of 256", n);
-    void *s = scratch(act_q8k_bytes(n, 1));
+    void *s = lib_scratch(act_q8k_bytes(n, 1));
     if (!s) return -1;
     ActQ8K a = act_q8k_view(s, n, 1);
     launch_quant_q8k(x_dev, n, 1, a, g_stream);
@@ -256,22 +269,33 @@ int aotk_quantize_q8_k(const float *x_dev, size_t n, aotk_block_q8_k *out_dev) {
 
 }  // extern "C"
 
-// Convert m reference-layout activation vectors into the plane layout in the
-// library scratch; returns the view to pass to launch_matvec.
-static int stage_act(const DevWeight &w, const void *x_dev, size_t m, ActQ8K &qk, ActQ8_0 &q0, const void *&act) {
+// Convert m reference-layout activation vectors into the plane layout;
+// returns the view to pass to launch_matvec. The staging memory is the
+// library scratch, or `fixed` (fixed_cap bytes) when that is given.
+static int stage_act(const DevWeight &w, const void *x_dev, size_t m, ActQ8K &qk, ActQ8_0 &q0, const void *&act,
+                     void *fixed = nullptr, size_t fixed_cap = 0) {
     int a = activation(w.kind);
-    if (a == ACT_Q8_K) {
-        void *s = scratch(act_q8k_bytes(w.cols, m));
-        if (!s) return -1;
-        qk = act_q8k_view(s, w.cols, m);
-        launch_ref_to_q8k((const aotk_block_q8_k *)x_dev, w.cols, m, qk, g_stream);
-        act = &qk;
-    } else if (a == ACT_Q8_0) {
-        void *s = scratch(act_q8_0_bytes(w.cols, m));
-        if (!s) return -1;
-        q0 = act_q8_0_view(s, w.cols, m);
-        launch_ref_to_q8_0((const aotk_block_q8_0 *)x_dev, w.cols, m, q0, g_stream);
-        act = &q0;
+    if (a == ACT_Q8_K || a == ACT_Q8_0) {
+        const size_t need = a == ACT_Q8_K ? act_q8k_bytes(w.cols, m) : act_q8_0_bytes(w.cols, m);
+        void *s;
+        if (fixed) {
+            if (need > fixed_cap)
+                return fail("matmul_noalloc: %zu inputs of %zu columns need %zu staging bytes, above the fixed %zu", m,
+                            w.cols, need, fixed_cap);
+            s = fixed;
+        } else {
+            s = lib_scratch(need);
+            if (!s) return -1;
+        }
+        if (a == ACT_Q8_K) {
+            qk = act_q8k_view(s, w.cols, m);
+            launch_ref_to_q8k((const aotk_block_q8_k *)x_dev, w.cols, m, qk, g_stream);
+            act = &qk;
+        } else {
+            q0 = act_q8_0_view(s, w.cols, m);
+            launch_ref_to_q8_0((const aotk_block_q8_0 *)x_dev, w.cols, m, q0, g_stream);
+            act = &q0;
+        }
     } else {
         act = x_dev;
     }
@@ -295,6 +319,20 @@ int aotk_matmul(const aotk_weight *w, const void *xs_dev, size_t m, float *out_d
     return 0;
 }
 
+int aotk_matmul_noalloc(const aotk_weight *w, const void *xs_dev, size_t m, float *out_dev) {
+    if (!w) return fail("null weight");
+    if (ensure_init()) return -1;
+    if (m == 0) return 0;
+    ActQ8K qk;
+    ActQ8_0 q0;
+    const void *act;
+    if (stage_act(w->dw, xs_dev, m, qk, q0, act, g_noalloc_scratch[g_device], NOALLOC_SCRATCH_BYTES)) return -1;
+    launch_matvec(w->dw, act, m, out_dev, nullptr, g_stream);
+    HIPC(hipGetLastError());
+    HIPC(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
 int aotk_matvec_f32(const aotk_weight *w, const float *x_dev, float *out_dev) {
     if (!w) return fail("null weight");
     const DevWeight &dw = w->dw;
@@ -303,13 +341,13 @@ int aotk_matvec_f32(const aotk_weight *w, const float *x_dev, float *out_dev) {
     ActQ8K qk;
     ActQ8_0 q0;
     if (a == ACT_Q8_K) {
-        void *s = scratch(act_q8k_bytes(dw.cols, 1));
+        void *s = lib_scratch(act_q8k_bytes(dw.cols, 1));
         if (!s) return -1;
         qk = act_q8k_view(s, dw.cols, 1);
         launch_quant_q8k(x_dev, dw.cols, 1, qk, g_stream);
         act = &qk;
     } else if (a == ACT_Q8_0) {
-        void *s = scratch(act_q8_0_bytes(dw.cols, 1));
+        void *s = lib_scratch(act_q8_0_bytes(dw.cols, 1));
         if (!s) return -1;
         q0 = act_q8_0_view(s, dw.cols, 1);
         launch_quant_q8_0(x_dev, dw.cols, 1, q0, g_stream);
@@ -383,7 +421,7 @@ int aotk_attention(float *out_dev, const float *q_dev, const float *k_cache_dev,
     if (ctx > 16384) return fail("attention: context %zu exceeds 16384 positions", ctx);
     size_t kv = n_kv_head * head_dim;
     size_t bytes = attention_scratch_bytes(n_head, head_dim, ctx, m);
-    void *s = scratch(bytes);
+    void *s = lib_scratch(bytes);
     if (!s) return -1;
     launch_attention(out_dev, q_dev, k_cache_dev + layer * ctx * kv, v_cache_dev + layer * ctx * kv, n_head, n_kv_head,
                      head_dim, ctx, pos0, m, window, nullptr, (float *)s, bytes, g_stream);
@@ -392,7 +430,7 @@ int aotk_attention(float *out_dev, const float *q_dev, const float *k_cache_dev,
 
 int aotk_argmax(const float *x_dev, size_t n, uint32_t *out_host) {
     if (ensure_init()) return -1;
-    uint8_t *s = (uint8_t *)scratch(4096);
+    uint8_t *s = (uint8_t *)lib_scratch(4096);
     if (!s) return -1;
     launch_argmax(x_dev, n, (uint32_t *)(s + 2048), (float *)s, g_stream);
     HIPC(hipGetLastError());
@@ -1361,7 +1399,7 @@ int aotk_time_matvec(const aotk_weight *const *ws, size_t n_w, const float *x_de
             return fail("time_matvec: weights differ in kind or shape");
     int a = activation(w0.kind);
     size_t act_bytes = a == ACT_Q8_K ? act_q8k_bytes(w0.cols, 1) : (a == ACT_Q8_0 ? act_q8_0_bytes(w0.cols, 1) : 0);
-    void *s = scratch(act_bytes + align_up(w0.rows * 4, 256));
+    void *s = lib_scratch(act_bytes + align_up(w0.rows * 4, 256));
     if (!s) return -1;
     float *y = (float *)((uint8_t *)s + act_bytes);
     ActQ8K qk;

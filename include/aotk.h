@@ -193,6 +193,17 @@ int aotk_matvec_f32(const aotk_weight *w, const float *x_dev, float *out_dev);
  * out_dev[i*rows + r]. Bit-identical to m calls of aotk_matvec. */
 int aotk_matmul(const aotk_weight *w, const void *xs_dev, size_t m, float *out_dev);
 
+/* aotk_matmul without any device allocation. No counterpart in the
+ * reference: for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The Q8_0 / Q8_K
+ * inputs are staged in a fixed 4 MiB device array of the library (one per
+ * GPU, held until the process ends) instead of the growable scratch; calls
+ * whose staging needs more (m * cols * ~1.14 bytes for Q8_K, ~1.13 for Q8_0,
+ * e.g. m = 64 at cols up to 28672) fail with -1. Results equal aotk_matmul's
+ * bit for bit. Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (from several threads) race. */
+int aotk_matmul_noalloc(const aotk_weight *w, const void *xs_dev, size_t m, float *out_dev);
+
 /* ------------------------------------------------------------------------ */
 /* Transformer operators (ops.rs)                                            */
 /* ------------------------------------------------------------------------ */
