@@ -1472,6 +1472,268 @@ static bool mv_half_fits(const MvArgs &a) {
     return true;
 }
 
+// ------------------------------------------- prompt matmul: Q8_0 family, floats
+// Batches of 2 or more tokens for the kinds whose reference kernels keep 8
+// f32 lanes (dot_*_q8_0 / dot_f16_f32 ..., simd_avx2.rs:58-129, 433-493, and
+// their x4 forms, :273-330, bit-identical to the singles). Lane = token (64
+// per grid row), wave = MQ_R weight rows, block = 4 waves. A wave's weights
+// are the same for all its lanes: scalar loads (s_load), the nibble unpacking
+// on the scalar unit. The activation tile of a stage (MQ_BS blocks of 32, or
+// 64 float elements, for 64 tokens) is staged in LDS, two stages in turn,
+// with the next stage's loads in flight during the current one. Per
+// (row, token) the 8 chains run in element order exactly as in the matvec
+// kernels, then the avx2 horizontal sum (and, for floats, the scalar tail):
+// a batch equals m matvecs bit for bit.
+constexpr int MQ_R = 4;   // rows per wave
+constexpr int MQ_BS = 8;  // 32-blocks (or 8-element groups x 8) per stage
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x8_t __attribute__((ext_vector_type(8)));
+
+// A load whose address is the same for every lane of the wave, through the
+// scalar data cache (read only).
+template <typename T>
+__device__ __forceinline__ T uload(const void *p) {
+    return *(const __attribute__((address_space(4))) T *)p;
+}
+
+// f16 element i of a uniform array of halves (4-byte aligned scalar load).
+__device__ __forceinline__ uint32_t uload_half(const uint16_t *base, size_t i) {
+    const uintptr_t at = (uintptr_t)(base + i);
+    const uint32_t v = uload<uint32_t>((const void *)(at & ~(uintptr_t)3));
+    return (at & 2) ? v >> 16 : v & 0xFFFFu;
+}
+
+__device__ __forceinline__ float hsum8(const float (&c)[8]) {
+    // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7))  (simd_avx2.rs:27-34)
+    return ((c[0] + c[4]) + (c[2] + c[6])) + ((c[1] + c[5]) + (c[3] + c[7]));
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void k_mm_q8(MvArgs a, int m) {
+    __shared__ __align__(16) uint8_t sx[2][MQ_BS][64][32];
+    __shared__ __align__(16) float sxd[2][MQ_BS][64];
+    constexpr int R = MQ_R;
+    constexpr int QB = KIND == AOTK_Q8_0 ? 32 : 16;  // quant bytes per block
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = blockIdx.y * 64;
+    const int nb = a.nb;
+    const int grow0 = (blockIdx.x * 4 + wave) * R;
+    const uint8_t *wq[R];
+    const uint16_t *wd[R];
+    const uint8_t *wh[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        int local;
+        const int sg = seg_of(a, grow0 + r < a.total_rows ? grow0 + r : 0, local);
+        wq[r] = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * nb * QB;
+        wd[r] = (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb;
+        wh[r] = KIND == AOTK_Q5_0 ? seg_sel(sg, a.w2[0], a.w2[1], a.w2[2]) + (size_t)local * nb * 4 : nullptr;
+    }
+    // stage loads: 64 tokens x MQ_BS blocks of 32 quants (4 quads per
+    // thread) and their scales (2 per thread); tokens past m and blocks past
+    // the end repeat the last (valid memory, never stored)
+    u32x4_t lx[4];
+    float lxd[2];
+    auto fetch = [&](int c0) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int j = tid + 256 * k;
+            const int t = min(t0 + (j >> 4), m - 1), b = min(c0 + ((j >> 1) & 7), nb - 1);
+            lx[k] = *(const u32x4_t *)(a.xq + (size_t)t * a.cols + (size_t)b * 32 + (j & 1) * 16);
+        }
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int j = tid + 256 * k;
+            const int t = min(t0 + (j >> 3), m - 1), b = min(c0 + (j & 7), nb - 1);
+            lxd[k] = a.xd[(size_t)t * nb + b];
+        }
+    };
+    auto put = [&](int st) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int j = tid + 256 * k;
+            *(u32x4_t *)&sx[st][(j >> 1) & 7][j >> 4][(j & 1) * 16] = lx[k];
+        }
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int j = tid + 256 * k;
+            sxd[st][j & 7][j >> 3] = lxd[k];
+        }
+    };
+    float acc[R][8];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int l = 0; l < 8; l++) acc[r][l] = 0.0f;
+    fetch(0);
+    put(0);
+    __syncthreads();
+    int st = 0;
+    for (int c0 = 0; c0 < nb; c0 += MQ_BS) {
+        const bool more = c0 + MQ_BS < nb;
+        if (more) fetch(c0 + MQ_BS);
+        const int n = nb - c0 < MQ_BS ? nb - c0 : MQ_BS;
+        for (int j = 0; j < n; j++) {
+            const int b = c0 + j;
+            const uint4 y0 = *(const uint4 *)&sx[st][j][lane][0], y1 = *(const uint4 *)&sx[st][j][lane][16];
+            const uint32_t yw[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+            const float yd = sxd[st][j][lane];
+            int off[8];
+#pragma unroll
+            for (int l = 0; l < 8; l++)
+                off[l] = KIND == AOTK_Q8_0 ? 0 : dot4(KIND == AOTK_Q5_0 ? 0xF0F0F0F0u : 0xF8F8F8F8u, yw[l], 0);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                uint32_t ww[8];
+                if (KIND == AOTK_Q8_0) {
+                    const u32x8_t v = uload<u32x8_t>(wq[r] + (size_t)b * 32);
+#pragma unroll
+                    for (int l = 0; l < 8; l++) ww[l] = v[l];
+                } else {
+                    const u32x4_t v = uload<u32x4_t>(wq[r] + (size_t)b * 16);
+                    uint32_t qh = 0;
+                    if (KIND == AOTK_Q5_0) qh = uload<uint32_t>(wh[r] + (size_t)b * 4);
+#pragma unroll
+                    for (int l = 0; l < 8; l++) {
+                        uint32_t q = l < 4 ? (v[l] & 0x0F0F0F0Fu) : ((v[l - 4] >> 4) & 0x0F0F0F0Fu);
+                        if (KIND == AOTK_Q5_0) {
+                            const uint32_t b4 = (qh >> (4 * l)) & 0xFu;
+                            const uint32_t spread = (b4 & 1u) | ((b4 & 2u) << 7) | ((b4 & 4u) << 14) | ((b4 & 8u) << 21);
+                            q |= spread << 4;
+                        }
+                        ww[l] = q;
+                    }
+                }
+                const float D = f16_to_f32(uload_half(wd[r], b)) * yd;
+#pragma unroll
+                for (int l = 0; l < 8; l++) acc[r][l] = fmaf(D, (float)dot4(ww[l], yw[l], off[l]), acc[r][l]);
+            }
+        }
+        if (more) {
+            put(st ^ 1);
+            __syncthreads();
+            st ^= 1;
+        }
+    }
+    const int tok = t0 + lane;
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        if (tok < m && grow0 + r < a.total_rows) store_row(a, grow0 + r, tok, hsum8(acc[r]));
+}
+
+// F16 / BF16 / F32 rows (4-byte aligned rows): stage = 64 elements x 64
+// tokens of f32 input.
+template <int KIND>
+__global__ __launch_bounds__(256) void k_mm_float(MvArgs a, int m) {
+    __shared__ __align__(16) float sx[2][8][64][8];  // [stage][group of 8][token][element]
+    constexpr int R = MQ_R;
+    constexpr int EB = KIND == AOTK_F32 ? 4 : 2;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = blockIdx.y * 64;
+    const int cols = (int)a.cols;
+    const int n8 = cols >> 3;
+    const int grow0 = (blockIdx.x * 4 + wave) * R;
+    const uint8_t *wr[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        int local;
+        const int sg = seg_of(a, grow0 + r < a.total_rows ? grow0 + r : 0, local);
+        wr[r] = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * a.rb;
+    }
+    // stage loads: 64 tokens x 64 elements, 16 floats per thread (runs of
+    // 64 consecutive elements: coalesced, any alignment); elements past the
+    // end repeat the last one (never used)
+    float lx[16];
+    auto fetch = [&](int g0) {
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int j = tid + 256 * k;  // (token j >> 6, element j & 63 of the stage)
+            const int t = min(t0 + (j >> 6), m - 1);
+            const int e = min(8 * g0 + (j & 63), cols - 1);
+            lx[k] = a.xf[(size_t)t * cols + e];
+        }
+    };
+    auto put = [&](int st) {
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int j = tid + 256 * k;
+            sx[st][(j & 63) >> 3][j >> 6][j & 7] = lx[k];
+        }
+    };
+    float acc[R][8];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int l = 0; l < 8; l++) acc[r][l] = 0.0f;
+    if (n8 > 0) {
+        fetch(0);
+        put(0);
+    }
+    __syncthreads();
+    int st = 0;
+    for (int g0 = 0; g0 < n8; g0 += 8) {
+        const bool more = g0 + 8 < n8;
+        if (more) fetch(g0 + 8);
+        const int n = n8 - g0 < 8 ? n8 - g0 : 8;
+        for (int j = 0; j < n; j++) {
+            const int g = g0 + j;
+            const float4 x0 = *(const float4 *)&sx[st][j][lane][0], x1 = *(const float4 *)&sx[st][j][lane][4];
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                float wv[8];
+                if (KIND == AOTK_F32) {
+                    const u32x8_t v = uload<u32x8_t>(wr[r] + (size_t)g * 32);
+#pragma unroll
+                    for (int l = 0; l < 8; l++) wv[l] = __uint_as_float(v[l]);
+                } else {
+                    const u32x4_t v = uload<u32x4_t>(wr[r] + (size_t)g * 16);
+#pragma unroll
+                    for (int l = 0; l < 8; l++) {
+                        const uint32_t h = (l & 1) ? v[l >> 1] >> 16 : v[l >> 1] & 0xFFFFu;
+                        wv[l] = KIND == AOTK_BF16 ? bf16_to_f32(h) : (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+                    }
+                }
+#pragma unroll
+                for (int l = 0; l < 8; l++) acc[r][l] = fmaf(wv[l], xv[l], acc[r][l]);
+            }
+        }
+        if (more) {
+            put(st ^ 1);
+            __syncthreads();
+            st ^= 1;
+        }
+    }
+    const int tok = t0 + lane;
+    const int tc = min(tok, m - 1);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float sum = hsum8(acc[r]);
+        for (int i = n8 * 8; i < cols; i++) {  // the scalar tail: sum += w * x
+            float w;
+            if (KIND == AOTK_F32) w = ((const float *)wr[r])[i];
+            else {
+                const uint32_t h = ((const uint16_t *)wr[r])[i];
+                w = KIND == AOTK_BF16 ? bf16_to_f32(h) : (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+            }
+            const float p = w * a.xf[(size_t)tc * cols + i];
+            sum = sum + p;
+        }
+        if (tok < m && grow0 + r < a.total_rows) store_row(a, grow0 + r, tok, sum);
+    }
+}
+
+static bool mm_float_fits(const MvArgs &a, int kind) {
+    const size_t eb = kind == AOTK_F32 ? 4 : 2;
+    if ((a.cols * eb) % 4 != 0) return false;
+    for (int i = 0; i < a.nseg; i++)
+        if ((uintptr_t)a.w[i] % 4 != 0) return false;
+    return true;
+}
+
 // ----------------------------------------------------------------- launch
 
 static size_t q8b_lds(const MvArgs &a) { return a.cols + a.cols / 32 * sizeof(float); }
@@ -1611,6 +1873,19 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
         default: MMK(AOTK_Q6_K) break;
         }
 #undef MMK
+        return;
+    }
+    if (m >= MM_MIN_TOKENS && (kind == AOTK_Q8_0 || kind == AOTK_Q4_0 || kind == AOTK_Q5_0 ||
+                               ((kind == AOTK_F16 || kind == AOTK_BF16 || kind == AOTK_F32) && mm_float_fits(a, kind)))) {
+        dim3 g((unsigned)((a.total_rows + 4 * MQ_R - 1) / (4 * MQ_R)), (unsigned)((m + 63) / 64));
+        switch (kind) {
+        case AOTK_Q8_0: k_mm_q8<AOTK_Q8_0><<<g, 256, 0, s>>>(a, (int)m); break;
+        case AOTK_Q4_0: k_mm_q8<AOTK_Q4_0><<<g, 256, 0, s>>>(a, (int)m); break;
+        case AOTK_Q5_0: k_mm_q8<AOTK_Q5_0><<<g, 256, 0, s>>>(a, (int)m); break;
+        case AOTK_F16: k_mm_float<AOTK_F16><<<g, 256, 0, s>>>(a, (int)m); break;
+        case AOTK_BF16: k_mm_float<AOTK_BF16><<<g, 256, 0, s>>>(a, (int)m); break;
+        default: k_mm_float<AOTK_F32><<<g, 256, 0, s>>>(a, (int)m); break;
+        }
         return;
     }
     switch (kind) {

@@ -134,6 +134,48 @@ def test_matmul_equals_matvec(aotk, oracle, kind):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("kind", ALL, ids=lambda k: NAMES[k])
+def test_matmul_batched_every_kind(aotk, oracle, kind):
+    """The batched prompt kernels of every kind (matvec.rs:524-546, the x4
+    kernels simd_avx2.rs:273-430) equal m matvecs bit for bit: ragged row
+    counts, batches past one 64-token grid row, odd float widths (scalar
+    tail), widths above 16384 columns."""
+    rng = np.random.default_rng(70 + kind)
+    widths = {F32: [8, 2053, 4096], F16: [64, 2053, 4104], BF16: [12, 2050, 4096], Q4_0: [32, 2048, 18432],
+              Q5_0: [96, 4096, 14336], Q8_0: [32, 4096, 18432], Q4_K: [256, 4096], Q5_K: [512, 2560], Q6_K: [256, 5632]}[kind]
+    for cols in widths:
+        rows = 75
+        raw = weights(kind, rows, cols, cols + kind, oracle)
+        w = aotk.Weight(kind, raw, rows, cols)
+        for m in (2, 17, 64, 100):
+            xs = [(rng.standard_normal(cols)).astype(np.float32) for _ in range(m)]
+            acts = np.concatenate([oracle.quantize_act(kind, x) for x in xs])
+            got = aotk.matmul(w, acts, m)
+            ref = oracle.matmul(kind, raw, acts, m, rows, cols, pool=oracle.Pool(8)).reshape(m, rows)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (cols, m)
+            if m == 17:  # and the matvec of one of the tokens
+                one = aotk.matvec(w, oracle.quantize_act(kind, xs[5]))
+                assert np.array_equal(one.view(np.uint32), ref[5].view(np.uint32)), cols
+        w.free()
+
+
+@pytest.mark.parametrize("kind,rows,cols", [(Q8_0, 6144, 4096), (Q8_0, 4096, 12288)], ids=["qkv", "down"])
+def test_matmul_qwen3_layer_chunk(aotk, oracle, kind, rows, cols):
+    """A 64-token prompt chunk through the Qwen3-8B Q8_0 layer shapes
+    (configs[3]; q/k/v fused to 6144 rows), bit-exact (509 rows tiled)."""
+    rng = np.random.default_rng(rows + cols)
+    m = 64
+    base = weights(kind, 509, cols, rows, oracle)
+    raw = np.resize(base, (rows, base.shape[1]))
+    w = aotk.Weight(kind, raw, rows, cols)
+    xs = [(rng.standard_normal(cols)).astype(np.float32) for _ in range(m)]
+    acts = np.concatenate([oracle.quantize_act(kind, x) for x in xs])
+    got = aotk.matmul(w, acts, m)
+    ref = oracle.matmul(kind, raw, acts, m, rows, cols, pool=oracle.Pool(16)).reshape(m, rows)
+    w.free()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("kind", [Q4_K, Q5_K, Q6_K], ids=lambda k: NAMES[k])
 def test_matmul_many_rows(aotk, oracle, kind):
     """2048 rows or more take the whole batch per 16-row block (super-blocks
