@@ -129,6 +129,9 @@ def load(path=None):
     _sig(lib, "aotk_matvec_f32", i, [vp, vp, vp])
     _sig(lib, "aotk_matmul", i, [vp, vp, sz, vp])
     _sig(lib, "aotk_matmul_noalloc", i, [vp, vp, sz, vp])
+    _sig(lib, "aotk_matvec3", i, [C.POINTER(vp), vp, C.POINTER(vp)])
+    _sig(lib, "aotk_matvec2", i, [vp, vp, vp, vp, vp])
+    _sig(lib, "aotk_matmul2", i, [vp, vp, vp, sz, vp, vp])
     _sig(lib, "aotk_rmsnorm", i, [vp, vp, vp, sz, sz, C.c_float])
     _sig(lib, "aotk_rmsnorm_heads", i, [vp, vp, sz, sz, C.c_float])
     _sig(lib, "aotk_rope", i, [vp, sz, sz, sz, sz, vp, i])

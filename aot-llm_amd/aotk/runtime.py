@@ -154,6 +154,33 @@ def matmul(w, xs_act, m):
     return out.to_numpy(np.float32).reshape(m, w.rows)
 
 
+def matvec3(ws, x_act):
+    """matvec3_*_input (matvec.rs:321-355): three matrices of one kind and
+    width over one pre-quantized input, one launch."""
+    dx = DeviceBuffer.from_numpy(np.ascontiguousarray(x_act))
+    outs = [DeviceBuffer(w.rows * 4) for w in ws]
+    warr = (C.c_void_p * 3)(*[w.h for w in ws])
+    oarr = (C.c_void_p * 3)(*[o.ptr for o in outs])
+    abi.check(_lib().aotk_matvec3(warr, dx.ptr, oarr))
+    return [o.to_numpy(np.float32) for o in outs]
+
+
+def matvec2(wa, wb, x_act):
+    """matvec2_*_input (matvec.rs:403-439): the gate/up pair."""
+    dx = DeviceBuffer.from_numpy(np.ascontiguousarray(x_act))
+    oa, ob = DeviceBuffer(wa.rows * 4), DeviceBuffer(wb.rows * 4)
+    abi.check(_lib().aotk_matvec2(wa.h, wb.h, dx.ptr, oa.ptr, ob.ptr))
+    return oa.to_numpy(np.float32), ob.to_numpy(np.float32)
+
+
+def matmul2(wa, wb, xs_act, m):
+    """matmul2_*_input (matvec.rs:569-583): the batched gate/up pair."""
+    dx = DeviceBuffer.from_numpy(np.ascontiguousarray(xs_act))
+    oa, ob = DeviceBuffer(m * wa.rows * 4), DeviceBuffer(m * wb.rows * 4)
+    abi.check(_lib().aotk_matmul2(wa.h, wb.h, dx.ptr, m, oa.ptr, ob.ptr))
+    return oa.to_numpy(np.float32).reshape(m, wa.rows), ob.to_numpy(np.float32).reshape(m, wb.rows)
+
+
 def matmul_noalloc(w, xs_act, m):
     """aotk_matmul_noalloc: the same product staged in the library's fixed
     device array (the caller's buffers are allocated here, the call itself

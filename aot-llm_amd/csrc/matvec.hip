@@ -1511,31 +1511,41 @@ __device__ __forceinline__ float hsum8(const float (&c)[8]) {
 
 template <int KIND>
 __global__ __launch_bounds__(256) void k_mm_q8(MvArgs a, int m) {
-    __shared__ __align__(16) uint8_t sx[2][MQ_BS][64][32];
-    __shared__ __align__(16) float sxd[2][MQ_BS][64];
     constexpr int R = MQ_R;
+    constexpr int WR = 4 * R;  // weight rows per block
+    static_assert(WR * MQ_BS == 128, "one (row, block) of the weight tile per thread of the first half");
+    // activation tile [stage][block][token][32 quants] and scales; weight
+    // tile [stage][row][block]: the block's 32 elements as signed bytes
+    // (Q4_0 / Q5_0 unpacked to q - 8 / q - 16 when staged) and f32(d)
+    __shared__ __align__(16) int8_t sx[2][MQ_BS][64][32];
+    __shared__ __align__(16) float sxd[2][MQ_BS][64];
+    __shared__ __align__(16) int8_t sw[2][WR][MQ_BS][32];
+    __shared__ __align__(16) float swd[2][WR][MQ_BS];
     constexpr int QB = KIND == AOTK_Q8_0 ? 32 : 16;  // quant bytes per block
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t0 = blockIdx.y * 64;
     const int nb = a.nb;
-    const int grow0 = (blockIdx.x * 4 + wave) * R;
-    const uint8_t *wq[R];
-    const uint16_t *wd[R];
-    const uint8_t *wh[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
+    const int row0 = blockIdx.x * WR;
+    // the (row, block) of the weight tile this thread stages (tid < 128)
+    const int wr_row = (tid >> 3) & (WR - 1), wr_blk = tid & 7;
+    const uint8_t *wq;
+    const uint16_t *wd;
+    const uint32_t *wh;
+    {
+        const int grow = row0 + wr_row;
         int local;
-        const int sg = seg_of(a, grow0 + r < a.total_rows ? grow0 + r : 0, local);
-        wq[r] = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * nb * QB;
-        wd[r] = (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb;
-        wh[r] = KIND == AOTK_Q5_0 ? seg_sel(sg, a.w2[0], a.w2[1], a.w2[2]) + (size_t)local * nb * 4 : nullptr;
+        const int sg = seg_of(a, grow < a.total_rows ? grow : a.total_rows - 1, local);
+        wq = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * nb * QB;
+        wd = (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb;
+        wh = KIND == AOTK_Q5_0 ? (const uint32_t *)seg_sel(sg, a.w2[0], a.w2[1], a.w2[2]) + (size_t)local * nb : nullptr;
     }
-    // stage loads: 64 tokens x MQ_BS blocks of 32 quants (4 quads per
-    // thread) and their scales (2 per thread); tokens past m and blocks past
-    // the end repeat the last (valid memory, never stored)
+    // stage loads (tokens past m and blocks past the end repeat the last:
+    // valid memory, never stored)
     u32x4_t lx[4];
     float lxd[2];
+    u32x4_t lw0, lw1;
+    uint32_t lwd = 0, lwh = 0;
     auto fetch = [&](int c0) {
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -1549,6 +1559,13 @@ __global__ __launch_bounds__(256) void k_mm_q8(MvArgs a, int m) {
             const int t = min(t0 + (j >> 3), m - 1), b = min(c0 + (j & 7), nb - 1);
             lxd[k] = a.xd[(size_t)t * nb + b];
         }
+        if (tid < 128) {
+            const int b = min(c0 + wr_blk, nb - 1);
+            lw0 = *(const u32x4_t *)(wq + (size_t)b * QB);
+            if (KIND == AOTK_Q8_0) lw1 = *(const u32x4_t *)(wq + (size_t)b * QB + 16);
+            if (KIND == AOTK_Q5_0) lwh = wh[b];
+            lwd = wd[b];
+        }
     };
     auto put = [&](int st) {
 #pragma unroll
@@ -1560,6 +1577,31 @@ __global__ __launch_bounds__(256) void k_mm_q8(MvArgs a, int m) {
         for (int k = 0; k < 2; k++) {
             const int j = tid + 256 * k;
             sxd[st][j & 7][j >> 3] = lxd[k];
+        }
+        if (tid < 128) {
+            u32x4_t lo = lw0, hi = lw1;
+            if (KIND != AOTK_Q8_0) {
+                // elements 0..15 are the low nibbles, 16..31 the high ones
+                // (quant.rs:300-443); as signed bytes q - 8 or q - 16
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    uint32_t l4 = lw0[i] & 0x0F0F0F0Fu, h4 = (lw0[i] >> 4) & 0x0F0F0F0Fu;
+                    if (KIND == AOTK_Q5_0) {
+                        const uint32_t bl = (lwh >> (4 * i)) & 0xFu, bh = (lwh >> (16 + 4 * i)) & 0xFu;
+                        l4 |= ((bl & 1u) | ((bl & 2u) << 7) | ((bl & 4u) << 14) | ((bl & 8u) << 21)) << 4;
+                        h4 |= ((bh & 1u) | ((bh & 2u) << 7) | ((bh & 4u) << 14) | ((bh & 8u) << 21)) << 4;
+                        // q - 16 per byte: q in 0..31, (q + 0xF0) mod 256 without carries between bytes
+                        lo[i] = ((l4 | 0x80808080u) - 0x10101010u) ^ 0x80808080u;
+                        hi[i] = ((h4 | 0x80808080u) - 0x10101010u) ^ 0x80808080u;
+                    } else {
+                        lo[i] = ((l4 | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+                        hi[i] = ((h4 | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+                    }
+                }
+            }
+            *(u32x4_t *)&sw[st][wr_row][wr_blk][0] = lo;
+            *(u32x4_t *)&sw[st][wr_row][wr_blk][16] = hi;
+            swd[st][wr_row][wr_blk] = f16_to_f32(lwd);
         }
     };
     float acc[R][8];
@@ -1576,51 +1618,33 @@ __global__ __launch_bounds__(256) void k_mm_q8(MvArgs a, int m) {
         if (more) fetch(c0 + MQ_BS);
         const int n = nb - c0 < MQ_BS ? nb - c0 : MQ_BS;
         for (int j = 0; j < n; j++) {
-            const int b = c0 + j;
-            const uint4 y0 = *(const uint4 *)&sx[st][j][lane][0], y1 = *(const uint4 *)&sx[st][j][lane][16];
-            const uint32_t yw[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+            const u32x4_t y0 = *(const u32x4_t *)&sx[st][j][lane][0], y1 = *(const u32x4_t *)&sx[st][j][lane][16];
             const float yd = sxd[st][j][lane];
-            int off[8];
-#pragma unroll
-            for (int l = 0; l < 8; l++)
-                off[l] = KIND == AOTK_Q8_0 ? 0 : dot4(KIND == AOTK_Q5_0 ? 0xF0F0F0F0u : 0xF8F8F8F8u, yw[l], 0);
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                uint32_t ww[8];
-                if (KIND == AOTK_Q8_0) {
-                    const u32x8_t v = uload<u32x8_t>(wq[r] + (size_t)b * 32);
+                // the same address in every lane: LDS broadcasts
+                const u32x4_t w0 = *(const u32x4_t *)&sw[st][R * wave + r][j][0];
+                const u32x4_t w1 = *(const u32x4_t *)&sw[st][R * wave + r][j][16];
+                const float D = swd[st][R * wave + r][j] * yd;
 #pragma unroll
-                    for (int l = 0; l < 8; l++) ww[l] = v[l];
-                } else {
-                    const u32x4_t v = uload<u32x4_t>(wq[r] + (size_t)b * 16);
-                    uint32_t qh = 0;
-                    if (KIND == AOTK_Q5_0) qh = uload<uint32_t>(wh[r] + (size_t)b * 4);
-#pragma unroll
-                    for (int l = 0; l < 8; l++) {
-                        uint32_t q = l < 4 ? (v[l] & 0x0F0F0F0Fu) : ((v[l - 4] >> 4) & 0x0F0F0F0Fu);
-                        if (KIND == AOTK_Q5_0) {
-                            const uint32_t b4 = (qh >> (4 * l)) & 0xFu;
-                            const uint32_t spread = (b4 & 1u) | ((b4 & 2u) << 7) | ((b4 & 4u) << 14) | ((b4 & 8u) << 21);
-                            q |= spread << 4;
-                        }
-                        ww[l] = q;
-                    }
+                for (int l = 0; l < 4; l++) {
+                    acc[r][l] = fmaf(D, (float)dot4(w0[l], y0[l], 0), acc[r][l]);
+                    acc[r][l + 4] = fmaf(D, (float)dot4(w1[l], y1[l], 0), acc[r][l + 4]);
                 }
-                const float D = f16_to_f32(uload_half(wd[r], b)) * yd;
-#pragma unroll
-                for (int l = 0; l < 8; l++) acc[r][l] = fmaf(D, (float)dot4(ww[l], yw[l], off[l]), acc[r][l]);
             }
         }
         if (more) {
-            put(st ^ 1);
+            put(st ^ 1);  // last read in the previous round, before its barrier
             __syncthreads();
             st ^= 1;
         }
     }
     const int tok = t0 + lane;
 #pragma unroll
-    for (int r = 0; r < R; r++)
-        if (tok < m && grow0 + r < a.total_rows) store_row(a, grow0 + r, tok, hsum8(acc[r]));
+    for (int r = 0; r < R; r++) {
+        const int grow = row0 + R * wave + r;
+        if (tok < m && grow < a.total_rows) store_row(a, grow, tok, hsum8(acc[r]));
+    }
 }
 
 // F16 / BF16 / F32 rows (4-byte aligned rows): stage = 64 elements x 64
@@ -1878,6 +1902,7 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
     if (m >= MM_MIN_TOKENS && (kind == AOTK_Q8_0 || kind == AOTK_Q4_0 || kind == AOTK_Q5_0 ||
                                ((kind == AOTK_F16 || kind == AOTK_BF16 || kind == AOTK_F32) && mm_float_fits(a, kind)))) {
         dim3 g((unsigned)((a.total_rows + 4 * MQ_R - 1) / (4 * MQ_R)), (unsigned)((m + 63) / 64));
+        // (k_mm_float keeps the same rows per block)
         switch (kind) {
         case AOTK_Q8_0: k_mm_q8<AOTK_Q8_0><<<g, 256, 0, s>>>(a, (int)m); break;
         case AOTK_Q4_0: k_mm_q8<AOTK_Q4_0><<<g, 256, 0, s>>>(a, (int)m); break;

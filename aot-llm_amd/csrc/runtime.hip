@@ -319,6 +319,52 @@ int aotk_matmul(const aotk_weight *w, const void *xs_dev, size_t m, float *out_d
     return 0;
 }
 
+// The fused multi-matrix products: one launch over the concatenated rows of
+// matrices of one kind and width sharing one input.
+static int multi_product(int n, const aotk_weight *const *ws, const void *xs_dev, size_t m, float *const *outs,
+                         const char *what, bool same_rows) {
+    for (int i = 0; i < n; i++)
+        if (!ws[i] || !outs[i]) return fail("%s: null weight or output", what);
+    const DevWeight &w0 = ws[0]->dw;
+    for (int i = 1; i < n; i++) {
+        const DevWeight &wi = ws[i]->dw;
+        if (wi.kind != w0.kind || wi.cols != w0.cols || (same_rows && wi.rows != w0.rows))
+            return fail("%s: the matrices differ in kind or shape", what);
+    }
+    if (m == 0) return 0;
+    ActQ8K qk;
+    ActQ8_0 q0;
+    const void *act;
+    if (stage_act(w0, xs_dev, m, qk, q0, act)) return -1;
+    const DevWeight *dws[3];
+    float *ys[3];
+    for (int i = 0; i < n; i++) {
+        dws[i] = &ws[i]->dw;
+        ys[i] = outs[i];
+    }
+    launch_matvec_multi(n, dws, ys, act, m, g_stream);
+    HIPC(hipGetLastError());
+    HIPC(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+int aotk_matvec3(const aotk_weight *const ws[3], const void *x_dev, float *const outs[3]) {
+    return multi_product(3, ws, x_dev, 1, outs, "matvec3", false);
+}
+
+int aotk_matvec2(const aotk_weight *w_a, const aotk_weight *w_b, const void *x_dev, float *out_a, float *out_b) {
+    const aotk_weight *ws[2] = {w_a, w_b};
+    float *outs[2] = {out_a, out_b};
+    return multi_product(2, ws, x_dev, 1, outs, "matvec2", true);
+}
+
+int aotk_matmul2(const aotk_weight *w_a, const aotk_weight *w_b, const void *xs_dev, size_t m, float *out_a,
+                 float *out_b) {
+    const aotk_weight *ws[2] = {w_a, w_b};
+    float *outs[2] = {out_a, out_b};
+    return multi_product(2, ws, xs_dev, m, outs, "matmul2", true);
+}
+
 int aotk_matmul_noalloc(const aotk_weight *w, const void *xs_dev, size_t m, float *out_dev) {
     if (!w) return fail("null weight");
     if (ensure_init()) return -1;

@@ -17,10 +17,11 @@ Also reported on the same JSON line:
   q4k_matvec     the Q4_K matvec kernel alone at the microbench shapes
                  (configs[1]), GB/s of algorithmic bytes, copies rotated past
                  the 256 MB Infinity Cache
-  matvec_kinds   the same for Q6_K at every shape and the other kinds at
-                 14336x4096
+  matvec_kinds   the same for the other seven kinds at every shape
   roofline       the dominant decode kernel (Q4_K matvec, 14336x4096) vs
                  MI355X HBM peak, timed with HIP events on the library stream
+  other_configs  Qwen3-8B Q8_0 (4096-token prefill, then 256 decode tokens) and
+                 Gemma-3-4B Q5_K_M (8192-token prefill, then 256 decode tokens)
   cpu_baseline   the CPU oracle (restated avx2+f16c reference kernels) on a
                  bounded sample of the same workload on this host's cores
 
@@ -67,10 +68,13 @@ def time_kernel(aotk, kind, rows, cols, iters=200, min_bytes=1 << 30):
     rb = rows * abi.row_bytes(kind, cols)
     copies = max(2, min(64, -(-min_bytes // rb)))
     rng = np.random.default_rng(1)
-    # encode one random matrix on the device, upload copies of its bytes
-    x = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
-    raw = aotk.quantize_rows(kind, x)
+    # 512 distinct rows of seeded N(0, 0.02) values encoded on the device,
+    # repeated to the full row count (the bytes streamed per launch are the
+    # full matrix's), uploaded as rotated copies
+    base = aotk.quantize_rows(kind, (rng.standard_normal((min(rows, 512), cols)) * 0.02).astype(np.float32))
+    raw = np.resize(base, (rows, base.shape[1]))
     ws = [aotk.Weight(kind, raw, rows, cols) for _ in range(copies)]
+    del raw
     xv = rng.standard_normal(cols).astype(np.float32)
     aotk.time_matvec(ws, xv, copies)  # warm-up
     ms = aotk.time_matvec(ws, xv, max(iters, copies))
@@ -79,33 +83,32 @@ def time_kernel(aotk, kind, rows, cols, iters=200, min_bytes=1 << 30):
     return ms, copies
 
 
-def extra_config(aotk, configs, name, n_ctx, steps):
-    """Decode tok/s of another benchmark config at its context: the KV cache
-    holds n_ctx positions (random values uploaded, standing in for the
-    prefill), then `steps` greedy forwards are timed."""
-    import numpy as np
+def extra_config(aotk, configs, name, n_ctx, steps, chunk=64):
+    """Another benchmark config as written: the KV cache prefilled by a
+    random-id prompt of n_ctx tokens through the batched prompt path
+    (app.rs:474-485, chunks of 64; timed: prefill tok/s), then `steps`
+    greedy decode forwards (timed: decode tok/s)."""
     spec = configs.build(name)
     model = aotk.Model(spec, seed=SEED)
-    d = spec.d
-    st = aotk.State(model, n_ctx + steps + 2, 1)
-    kv = d["n_kv_head"] * d["head_dim"]
-    rng = np.random.default_rng(1)
-    k = (rng.standard_normal((d["n_layer"], n_ctx, kv)) * 0.5).astype(np.float32)
-    v = rng.standard_normal((d["n_layer"], n_ctx, kv)).astype(np.float32)
-    st.kv_upload(n_ctx, k, v)
-    del k, v
-    st.forward(1, n_ctx, True)
-    st.generate(n_ctx + 1, 4)  # warm-up (and graph capture)
+    st = aotk.State(model, n_ctx + steps + 2, chunk)
+    toks = configs.prompt_tokens(2, n_ctx, spec.d["vocab"])
     aotk.sync()
     t = time.perf_counter()
-    st.generate(n_ctx + 1, steps + 1)
+    st.prompt(toks, batch=chunk)
+    aotk.sync()
+    t_pre = time.perf_counter() - t
+    st.generate(n_ctx, 2)  # warm-up (and graph capture) at the next position
+    aotk.sync()
+    t = time.perf_counter()
+    gen = st.generate(n_ctx, steps + 1)
     aotk.sync()
     dt = time.perf_counter() - t
     wb = model.weight_bytes()
     st.free()
     model.free()
-    return dict(decode_tok_s=round(steps / dt, 2), context=n_ctx, steps=steps, weight_GB=round(wb / 1e9, 3),
-                note="KV cache of random values at the given context, then greedy decode")
+    return dict(decode_tok_s=round(steps / dt, 2), prefill_tok_s=round(n_ctx / t_pre, 1), prefill_s=round(t_pre, 3),
+                context=n_ctx, steps=steps, weight_GB=round(wb / 1e9, 3), greedy_head=gen[:4],
+                note=f"{n_ctx}-token random-id prompt in {chunk}-token chunks, then {steps} greedy decode tokens")
 
 
 def measured_traffic(kernel):
@@ -121,34 +124,49 @@ def measured_traffic(kernel):
     return t.get("traffic_bytes") if t.get("kernel") == kernel else None
 
 
-def cpu_baseline(spec, blob, n_prompt, budget_s):
-    """Oracle forward on host cores: a short prompt, then decode until the
-    time budget is spent; tok/s like the reference's stats line."""
+def cpu_baseline(spec, blob, n_prompt, chunk, budget_s):
+    """The oracle (the restated avx2+f16c kernels) on this host's cores, on
+    the same workload as the GPU line: the same n_prompt-token prompt in
+    chunks of `chunk` (timed: prompt tok/s), then greedy decode from
+    position n_prompt until the time budget is spent, with the reference's
+    default thread count min(cores, 8) (app.rs:214-216); then the same decode
+    for half the budget on all cores. tok/s as the reference's stats line."""
     from oracle import oracle as O
     from aotk import configs
-    threads = min(os.cpu_count() or 1, 8)  # app.rs:214-216 default
-    ctx = n_prompt + 256
-    m = O.Model(spec, blob, ctx, max_batch=64, n_threads=threads, kernels=1)
-    toks = configs.prompt_tokens(1, n_prompt, spec.d["vocab"])
-    t = time.perf_counter()
-    m.prompt(toks, batch=64)
-    tp = time.perf_counter() - t
-    pos = n_prompt
-    tok = O.argmax(m.logits())
-    n = 0
-    t = time.perf_counter()
-    while time.perf_counter() - t < budget_s and n < 200:
-        m.forward(tok, pos, True)
+    cores = os.cpu_count() or 1
+
+    def decode(m, threads, budget):
         tok = O.argmax(m.logits())
-        pos += 1
-        n += 1
-    tg = time.perf_counter() - t
+        pos, n = n_prompt, 0
+        t = time.perf_counter()
+        while time.perf_counter() - t < budget and n < 400:
+            m.forward(tok, pos, True)
+            tok = O.argmax(m.logits())
+            pos += 1
+            n += 1
+        return n, time.perf_counter() - t
+
+    threads = min(cores, 8)
+    ctx = n_prompt + 420
+    toks = configs.prompt_tokens(1, n_prompt, spec.d["vocab"])
+    m = O.Model(spec, blob, ctx, max_batch=chunk, n_threads=threads, kernels=1)
+    t = time.perf_counter()
+    m.prompt(toks, batch=chunk)
+    tp = time.perf_counter() - t
+    n, tg = decode(m, threads, budget_s)
     m.close()
+    all_cores = None
+    if cores > threads:
+        m = O.Model(spec, blob, ctx, max_batch=chunk, n_threads=cores, kernels=1)
+        m.prompt(toks, batch=chunk)
+        n2, tg2 = decode(m, cores, budget_s / 2)
+        m.close()
+        all_cores = dict(decode_tok_s=round(n2 / tg2, 3), threads=cores)
     return dict(value=round(n / tg, 3), unit="tok/s", cores=threads, kind="port",
-                sample=f"{spec.cfg.get('name', 'llama3-8b-q4km')}: {n_prompt}-token prompt "
-                       f"({n_prompt / tp:.2f} prompt tok/s) then {n} greedy decode forwards at positions "
-                       f"{n_prompt}..{pos - 1}, avx2+f16c kernels, {threads} threads",
-                host_cpu=cpu_model(), host_cores=os.cpu_count(), prompt_tok_s=round(n_prompt / tp, 3))
+                sample=f"{spec.cfg.get('name', 'llama3-8b-q4km')}: the same {n_prompt}-token prompt in {chunk}-token "
+                       f"chunks ({n_prompt / tp:.2f} prompt tok/s), then {n} greedy decode forwards at positions "
+                       f"{n_prompt}..{n_prompt + n - 1}, avx2+f16c kernels, {threads} threads",
+                host_cpu=cpu_model(), host_cores=cores, prompt_tok_s=round(n_prompt / tp, 3), all_cores=all_cores)
 
 
 def micro_only():
@@ -173,7 +191,8 @@ def main():
     ap.add_argument("--config", default="llama3-8b-q4km")
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--chunk", type=int, default=64)
-    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--extra-steps", type=int, default=256, help="decode tokens of the Qwen3 / Gemma-3 lines")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-micro", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the Qwen3 / Gemma-3 decode lines")
@@ -242,10 +261,9 @@ def main():
 
         for rows, cols in shapes:
             micro[f"{rows}x{cols}"] = measure(abi.Q4_K, rows, cols)
-        # Q6_K at every shape, the other kinds at the ffn shape
-        kinds_micro["q6_K"] = {f"{r}x{c}": measure(abi.Q6_K, r, c) for r, c in shapes}
-        for kind in (abi.Q5_K, abi.Q8_0, abi.Q4_0, abi.Q5_0, abi.F16, abi.BF16):
-            kinds_micro[abi.KIND_NAMES[kind]] = {"14336x4096": measure(kind, 14336, 4096)}
+        # every other kind at every shape
+        for kind in (abi.Q6_K, abi.Q5_K, abi.Q8_0, abi.Q4_0, abi.Q5_0, abi.F16, abi.BF16):
+            kinds_micro[abi.KIND_NAMES[kind]] = {f"{r}x{c}": measure(kind, r, c) for r, c in shapes}
         dom = micro["14336x4096"]
         roofline = dict(bound="hbm", achieved=dom["GBs"], peak=HBM_PEAK_GBS, unit="GB/s", frac=dom["frac"],
                         traffic=measured_traffic("k_mv_kq<Q4_K> 14336x4096"),
@@ -255,15 +273,16 @@ def main():
     extra = {}
     if not a.no_extra:
         for name, n_ctx in (("qwen3-8b-q8_0", 4096), ("gemma3-4b-q5km", 8192)):
-            extra[name] = extra_config(aotk, configs, name, n_ctx, 64)
-            log(f"{name}: {extra[name]['decode_tok_s']} tok/s decode at {n_ctx} context")
+            extra[name] = extra_config(aotk, configs, name, n_ctx, a.extra_steps)
+            log(f"{name}: prefill {n_ctx} tokens {extra[name]['prefill_tok_s']} tok/s, "
+                f"{extra[name]['decode_tok_s']} tok/s decode at {n_ctx}+ context")
 
     cpu = None
     if not a.no_cpu:
         log("cpu baseline: downloading the weights and running the oracle ...")
         blob = model.download()
         st.free()
-        cpu = cpu_baseline(spec, blob, 8, a.cpu_seconds)
+        cpu = cpu_baseline(spec, blob, a.prompt, a.chunk, a.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads ({cpu['host_cpu']})")
 
     line = {

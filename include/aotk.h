@@ -193,6 +193,21 @@ int aotk_matvec_f32(const aotk_weight *w, const float *x_dev, float *out_dev);
  * out_dev[i*rows + r]. Bit-identical to m calls of aotk_matvec. */
 int aotk_matmul(const aotk_weight *w, const void *xs_dev, size_t m, float *out_dev);
 
+/* Fused products sharing one input, each one launch over the concatenated
+ * rows (the reference's single parallel region):
+ * aotk_matvec3: `matvec3_q8_k_input` / `matvec3_q8_0_input` (matvec.rs:321-355),
+ *   the q/k/v projections: three matrices of one kind and width, rows may
+ *   differ; outs[i][r] = dot(row r of ws[i], x).
+ * aotk_matvec2: `matvec2_q8_k_input` / `matvec2_q8_0_input` (matvec.rs:403-439),
+ *   the gate/up pair: two matrices of one kind and shape.
+ * aotk_matmul2: `matmul2_q8_k_input` / `matmul2_q8_0_input` (matvec.rs:569-583),
+ *   the batched pair: out_a[i*rows + r], out_b[i*rows + r] for m inputs.
+ * Inputs in the formats of aotk_matvec / aotk_matmul; results equal the
+ * separate products bit for bit. */
+int aotk_matvec3(const aotk_weight *const ws[3], const void *x_dev, float *const outs[3]);
+int aotk_matvec2(const aotk_weight *w_a, const aotk_weight *w_b, const void *x_dev, float *out_a, float *out_b);
+int aotk_matmul2(const aotk_weight *w_a, const aotk_weight *w_b, const void *xs_dev, size_t m, float *out_a, float *out_b);
+
 /* aotk_matmul without any device allocation. No counterpart in the
  * reference: for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). The Q8_0 / Q8_K

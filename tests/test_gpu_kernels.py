@@ -351,3 +351,33 @@ def test_exact_sequential_sum_softmax(aotk, oracle, n):
         ref = s.copy()
         oracle.load().or_softmax(oracle.ptr(ref), ref.size)
         assert np.array_equal(aotk.softmax(s).view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", [Q4_K, Q6_K, Q8_0, Q4_0, F16, F32], ids=lambda k: NAMES[k])
+def test_fused_products(aotk, oracle, kind):
+    """aotk_matvec3 / aotk_matvec2 / aotk_matmul2 (matvec.rs:321-439,
+    :569-583): one launch over the concatenated rows, each output equal to
+    its own product bit for bit."""
+    rng = np.random.default_rng(90 + kind)
+    cols = 1024
+    shapes = [(96, cols), (32, cols), (40, cols)]
+    raws = [weights(kind, r, c, 50 + i, oracle) for i, (r, c) in enumerate(shapes)]
+    ws = [aotk.Weight(kind, raw, r, c) for raw, (r, c) in zip(raws, shapes)]
+    x = rng.standard_normal(cols).astype(np.float32)
+    act = oracle.quantize_act(kind, x)
+    got = aotk.matvec3(ws, act)
+    for g, raw, (r, c) in zip(got, raws, shapes):
+        ref = oracle.matvec(kind, raw, act, r, c)
+        assert np.array_equal(g.view(np.uint32), ref.view(np.uint32))
+    ub = weights(kind, 96, cols, 77, oracle)
+    wb = aotk.Weight(kind, ub, 96, cols)
+    ga, gb = aotk.matvec2(ws[0], wb, act)
+    assert np.array_equal(ga.view(np.uint32), oracle.matvec(kind, raws[0], act, 96, cols).view(np.uint32))
+    assert np.array_equal(gb.view(np.uint32), oracle.matvec(kind, ub, act, 96, cols).view(np.uint32))
+    for m in (5, 64):
+        xs = np.concatenate([oracle.quantize_act(kind, rng.standard_normal(cols).astype(np.float32)) for _ in range(m)])
+        ma, mb = aotk.matmul2(ws[0], wb, xs, m)
+        assert np.array_equal(ma.view(np.uint32), oracle.matmul(kind, raws[0], xs, m, 96, cols).reshape(m, 96).view(np.uint32))
+        assert np.array_equal(mb.view(np.uint32), oracle.matmul(kind, ub, xs, m, 96, cols).reshape(m, 96).view(np.uint32))
+    with pytest.raises(aotk.AotkError, match="differ"):
+        aotk.matvec2(ws[0], ws[1], act)
