@@ -23,6 +23,9 @@ FLAGS = [
     "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
     # never emit packed-FP32 VALU ops (they are avoided on this pool)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # matrix-core results in VGPRs (the f32 folds read them directly; the
+    # AGPR form costs one v_accvgpr_read per value)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-result",
 ]
 

@@ -59,8 +59,9 @@ struct ActQ8K {
     int16_t *bsums;  // [rows][n/16]
 };
 struct ActQ8_0 {
-    int8_t *qs;  // [rows][n]
-    float *d;    // [rows][n/32]
+    int8_t *qs;     // [rows][n]
+    float *d;       // [rows][n/32]
+    uint16_t *xh;   // [rows][n] the quants as f16 (filled for batched products)
 };
 
 // Bytes of an activation buffer for `rows` vectors of n elements.
@@ -77,13 +78,17 @@ inline ActQ8K act_q8k_view(void *base, size_t n, size_t rows) {
     a.bsums = (int16_t *)p;
     return a;
 }
-inline size_t act_q8_0_bytes(size_t n, size_t rows) { return align_up(rows * n, 256) + align_up(rows * (n / 32) * 4, 256); }
+inline size_t act_q8_0_bytes(size_t n, size_t rows) {
+    return align_up(rows * n, 256) + align_up(rows * (n / 32) * 4, 256) + align_up(rows * n * 2, 256);
+}
 inline ActQ8_0 act_q8_0_view(void *base, size_t n, size_t rows) {
     uint8_t *p = (uint8_t *)base;
     ActQ8_0 a;
     a.qs = (int8_t *)p;
     p += align_up(rows * n, 256);
     a.d = (float *)p;
+    p += align_up(rows * (n / 32) * 4, 256);
+    a.xh = (uint16_t *)p;
     return a;
 }
 

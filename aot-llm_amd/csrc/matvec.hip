@@ -41,6 +41,7 @@ struct MvArgs {
     const float *xd;
     const int16_t *xbs;
     const float *xf;
+    uint16_t *xh;  // Q8_0 family, batches: the quants as f16 (written before the matmul)
     // K-quant rows, one token: when set, every block quantizes this f32
     // input to Q8_K itself (instead of reading xq / xd / xbs)
     const float *xq_src;
@@ -1484,8 +1485,7 @@ static bool mv_half_fits(const MvArgs &a) {
 // (row, token) the 8 chains run in element order exactly as in the matvec
 // kernels, then the avx2 horizontal sum (and, for floats, the scalar tail):
 // a batch equals m matvecs bit for bit.
-constexpr int MQ_R = 4;   // rows per wave
-constexpr int MQ_BS = 8;  // 32-blocks (or 8-element groups x 8) per stage
+constexpr int MQ_R = 4;  // rows per wave of k_mm_float
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x8_t __attribute__((ext_vector_type(8)));
@@ -1509,141 +1509,240 @@ __device__ __forceinline__ float hsum8(const float (&c)[8]) {
     return ((c[0] + c[4]) + (c[2] + c[6])) + ((c[1] + c[5]) + (c[3] + c[7]));
 }
 
-template <int KIND>
+// Q8_0 / Q4_0 / Q5_0 on the f16 matrix cores. The reference's integer part
+// per block is, for each of the 8 lanes of its accumulator, a sum of 4
+// consecutive products P_l (exact: |q| <= 127, |P_l| <= 64516). Here one
+// v_mfma_f32_16x16x32_f16 forms P for 4 rows x 16 tokens x 4 of the 8
+// groups: A holds the 4 rows' block in group-diagonal form (M index 4r + i
+// carries group 2i, or 2i + 1 in the odd product, every other entry zero),
+// B the 16 tokens' activations; the values are integers exact in f16 and
+// every partial sum is an integer below 2^24, so the f32 result is P itself.
+// Lane (q, n) then owns the 8 chains of row q and token n: the f32 fold
+// acc_l = fma(f16(d) * y.d, P_l, acc_l) over blocks in order and the avx2
+// horizontal sum run on the VALU exactly as in the matvec.
+// Wave = SETS sets of 4 rows x TILES tiles of 16 tokens; block = 4 waves
+// over BR rows x 64 tokens. The activations arrive as f16 (k_q8_to_f16,
+// once per batch), the weights are converted to f16 when staged; both are
+// staged in LDS, MQ_BS blocks per stage, two stages in LDS and two more in
+// registers in flight.
+constexpr int MQ_BS = 2;   // blocks of 32 per stage
+constexpr int MQ_XS = 40;  // halves per (block, token) line of the activation tile (32 + pad)
+
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+// four unsigned bytes u_i -> the f16 values u_i - bias (exact for u, bias < 1024)
+__device__ __forceinline__ void u8x4_to_f16(uint32_t u, float bias, uint32_t &lo, uint32_t &hi) {
+    // 0x64 above each byte: the half 1024 + u_i
+    const uint32_t l = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const h2_t off = {(_Float16)(-1024.0f - bias), (_Float16)(-1024.0f - bias)};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, l) + off);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, h) + off);
+}
+
+// The batch's int8 quants as f16 (16 per thread).
+__global__ __launch_bounds__(256) void k_q8_to_f16(const int8_t *__restrict__ xq, uint16_t *__restrict__ xh, size_t n16) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n16) return;
+    const u32x4_t v = ((const u32x4_t *)xq)[i];
+    uint32_t h[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) u8x4_to_f16(v[k] ^ 0x80808080u, 128.0f, h[2 * k], h[2 * k + 1]);
+    ((u32x4_t *)xh)[2 * i] = u32x4_t{h[0], h[1], h[2], h[3]};
+    ((u32x4_t *)xh)[2 * i + 1] = u32x4_t{h[4], h[5], h[6], h[7]};
+}
+
+template <int KIND, int SETS, int TILES>
 __global__ __launch_bounds__(256) void k_mm_q8(MvArgs a, int m) {
-    constexpr int R = MQ_R;
-    constexpr int WR = 4 * R;  // weight rows per block
-    static_assert(WR * MQ_BS == 128, "one (row, block) of the weight tile per thread of the first half");
-    // activation tile [stage][block][token][32 quants] and scales; weight
-    // tile [stage][row][block]: the block's 32 elements as signed bytes
-    // (Q4_0 / Q5_0 unpacked to q - 8 / q - 16 when staged) and f32(d)
-    __shared__ __align__(16) int8_t sx[2][MQ_BS][64][32];
-    __shared__ __align__(16) float sxd[2][MQ_BS][64];
-    __shared__ __align__(16) int8_t sw[2][WR][MQ_BS][32];
-    __shared__ __align__(16) float swd[2][WR][MQ_BS];
+    constexpr int WTW = 4 / TILES;      // waves along the tokens
+    constexpr int WRW = 4 / WTW;        // waves along the rows
+    constexpr int BR = WRW * 4 * SETS;  // weight rows per block
     constexpr int QB = KIND == AOTK_Q8_0 ? 32 : 16;  // quant bytes per block
+    constexpr int WPT = KIND == AOTK_Q8_0 ? 2 : 1;   // 16-byte quant loads per (row, block)
+    constexpr int WT = BR * MQ_BS * WPT;             // weight staging threads
+    static_assert(WT <= 256, "weight tile");
+    __shared__ __align__(16) _Float16 sx[2][MQ_BS][64][MQ_XS];  // activations
+    __shared__ __align__(16) float sxd[2][MQ_BS][64];           // their scales
+    __shared__ __align__(16) _Float16 sw[2][BR][MQ_BS][32];     // weight quants
+    __shared__ __align__(16) float swd[2][BR][MQ_BS];           // f32(d)
+    __shared__ __align__(16) _Float16 szero[8];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wave / WTW, wt = wave % WTW;
     const int t0 = blockIdx.y * 64;
     const int nb = a.nb;
-    const int row0 = blockIdx.x * WR;
-    // the (row, block) of the weight tile this thread stages (tid < 128)
-    const int wr_row = (tid >> 3) & (WR - 1), wr_blk = tid & 7;
+    const int row0 = blockIdx.x * BR;
+    const int mt = min(64, m - t0);
+    if (tid < 4) ((uint32_t *)szero)[tid] = 0u;
+    // the weight row / block / 16-byte part this thread stages
+    const int w_part = tid % WPT, w_blk = (tid / WPT) % MQ_BS, w_row = min(tid / (WPT * MQ_BS), BR - 1);
     const uint8_t *wq;
     const uint16_t *wd;
     const uint32_t *wh;
     {
-        const int grow = row0 + wr_row;
+        const int grow = min(row0 + w_row, a.total_rows - 1);
         int local;
-        const int sg = seg_of(a, grow < a.total_rows ? grow : a.total_rows - 1, local);
+        const int sg = seg_of(a, grow, local);
         wq = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * nb * QB;
         wd = (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb;
         wh = KIND == AOTK_Q5_0 ? (const uint32_t *)seg_sel(sg, a.w2[0], a.w2[1], a.w2[2]) + (size_t)local * nb : nullptr;
     }
     // stage loads (tokens past m and blocks past the end repeat the last:
     // valid memory, never stored)
-    u32x4_t lx[4];
-    float lxd[2];
-    u32x4_t lw0, lw1;
-    uint32_t lwd = 0, lwh = 0;
-    auto fetch = [&](int c0) {
+    struct Ld {
+        u32x4_t x[2], w;
+        float xd;
+        uint32_t wd, wh;
+    };
+    Ld L[2];
+    auto fetch = [&](Ld &ld, int c0) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int j = tid + 256 * k;
-            const int t = min(t0 + (j >> 4), m - 1), b = min(c0 + ((j >> 1) & 7), nb - 1);
-            lx[k] = *(const u32x4_t *)(a.xq + (size_t)t * a.cols + (size_t)b * 32 + (j & 1) * 16);
+        for (int k = 0; k < 2; k++) {  // 64 tokens x 2 blocks x 4 parts of 16 bytes
+            const int c = tid + 256 * k;
+            const int t = min(t0 + (c >> 3), m - 1), b = min(c0 + ((c >> 2) & 1), nb - 1);
+            ld.x[k] = *(const u32x4_t *)(a.xh + (size_t)t * a.cols + (size_t)b * 32 + (c & 3) * 8);
         }
-#pragma unroll
-        for (int k = 0; k < 2; k++) {
-            const int j = tid + 256 * k;
-            const int t = min(t0 + (j >> 3), m - 1), b = min(c0 + (j & 7), nb - 1);
-            lxd[k] = a.xd[(size_t)t * nb + b];
+        if (tid < 64 * MQ_BS) {
+            const int t = min(t0 + (tid >> 1), m - 1), b = min(c0 + (tid & 1), nb - 1);
+            ld.xd = a.xd[(size_t)t * nb + b];
         }
-        if (tid < 128) {
-            const int b = min(c0 + wr_blk, nb - 1);
-            lw0 = *(const u32x4_t *)(wq + (size_t)b * QB);
-            if (KIND == AOTK_Q8_0) lw1 = *(const u32x4_t *)(wq + (size_t)b * QB + 16);
-            if (KIND == AOTK_Q5_0) lwh = wh[b];
-            lwd = wd[b];
+        if (tid < WT) {
+            const int b = min(c0 + w_blk, nb - 1);
+            ld.w = *(const u32x4_t *)(wq + (size_t)b * QB + w_part * 16);
+            if (KIND == AOTK_Q5_0) ld.wh = wh[b];
+            if (w_part == 0) ld.wd = wd[b];
         }
     };
-    auto put = [&](int st) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int j = tid + 256 * k;
-            *(u32x4_t *)&sx[st][(j >> 1) & 7][j >> 4][(j & 1) * 16] = lx[k];
-        }
+    auto put = [&](const Ld &ld, int st) {
 #pragma unroll
         for (int k = 0; k < 2; k++) {
-            const int j = tid + 256 * k;
-            sxd[st][j & 7][j >> 3] = lxd[k];
+            const int c = tid + 256 * k;
+            *(u32x4_t *)&sx[st][(c >> 2) & 1][c >> 3][(c & 3) * 8] = ld.x[k];
         }
-        if (tid < 128) {
-            u32x4_t lo = lw0, hi = lw1;
-            if (KIND != AOTK_Q8_0) {
-                // elements 0..15 are the low nibbles, 16..31 the high ones
-                // (quant.rs:300-443); as signed bytes q - 8 or q - 16
+        if (tid < 64 * MQ_BS) sxd[st][tid & 1][tid >> 1] = ld.xd;
+        if (tid < WT) {
+            uint32_t *dst = (uint32_t *)&sw[st][w_row][w_blk][w_part * 16];
+            if (KIND == AOTK_Q8_0) {
+                uint32_t h[8];
+#pragma unroll
+                for (int i = 0; i < 4; i++) u8x4_to_f16(ld.w[i] ^ 0x80808080u, 128.0f, h[2 * i], h[2 * i + 1]);
+                *(u32x4_t *)dst = u32x4_t{h[0], h[1], h[2], h[3]};
+                *(u32x4_t *)(dst + 4) = u32x4_t{h[4], h[5], h[6], h[7]};
+            } else {
+                // elements 0..15: low nibbles, 16..31: high nibbles (quant.rs:300-443)
+                uint32_t h[16];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    uint32_t l4 = lw0[i] & 0x0F0F0F0Fu, h4 = (lw0[i] >> 4) & 0x0F0F0F0Fu;
+                    uint32_t l4 = ld.w[i] & 0x0F0F0F0Fu, h4 = (ld.w[i] >> 4) & 0x0F0F0F0Fu;
                     if (KIND == AOTK_Q5_0) {
-                        const uint32_t bl = (lwh >> (4 * i)) & 0xFu, bh = (lwh >> (16 + 4 * i)) & 0xFu;
+                        const uint32_t bl = (ld.wh >> (4 * i)) & 0xFu, bh = (ld.wh >> (16 + 4 * i)) & 0xFu;
                         l4 |= ((bl & 1u) | ((bl & 2u) << 7) | ((bl & 4u) << 14) | ((bl & 8u) << 21)) << 4;
                         h4 |= ((bh & 1u) | ((bh & 2u) << 7) | ((bh & 4u) << 14) | ((bh & 8u) << 21)) << 4;
-                        // q - 16 per byte: q in 0..31, (q + 0xF0) mod 256 without carries between bytes
-                        lo[i] = ((l4 | 0x80808080u) - 0x10101010u) ^ 0x80808080u;
-                        hi[i] = ((h4 | 0x80808080u) - 0x10101010u) ^ 0x80808080u;
-                    } else {
-                        lo[i] = ((l4 | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
-                        hi[i] = ((h4 | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+                    }
+                    const float bias = KIND == AOTK_Q5_0 ? 16.0f : 8.0f;
+                    u8x4_to_f16(l4, bias, h[2 * i], h[2 * i + 1]);
+                    u8x4_to_f16(h4, bias, h[8 + 2 * i], h[8 + 2 * i + 1]);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) *(u32x4_t *)(dst + 4 * i) = u32x4_t{h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]};
+            }
+            if (w_part == 0) swd[st][w_row][w_blk] = f16_to_f32(ld.wd);
+        }
+    };
+    // lane roles: q = lane / 16 (the output row in a set of 4, and the
+    // operands' k-quarter), n = lane % 16 (the token in a tile; as an A row
+    // index, row n / 4 of the set with group pair n % 4)
+    const int q = lane >> 4, n = lane & 15;
+    const bool a_on = (n & 3) == q;  // A[4r + i][k] is nonzero only in k-quarter i
+    const int a_row = n >> 2;
+    f4_t acc[SETS][TILES][2];  // [row set][token tile][even / odd groups]
+#pragma unroll
+    for (int s = 0; s < SETS; s++)
+#pragma unroll
+        for (int t = 0; t < TILES; t++) acc[s][t][0] = acc[s][t][1] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    fetch(L[0], 0);
+    if (MQ_BS < nb) fetch(L[1], MQ_BS);
+    put(L[0], 0);
+    __syncthreads();
+    // one stage: stage c0 + 2 * MQ_BS goes into the register set `fr` just
+    // emptied, the stage in `pr` (fetched a round earlier) into the other
+    // LDS buffer after the compute (last read in the previous round, before
+    // its barrier)
+    auto round = [&](int c0, int st, Ld &fr, const Ld &pr) {
+        if (c0 + 2 * MQ_BS < nb) fetch(fr, c0 + 2 * MQ_BS);
+        const int nblk = nb - c0 < MQ_BS ? nb - c0 : MQ_BS;
+        for (int j = 0; j < nblk; j++) {
+            h8_t bx[TILES];
+            float yd[TILES];
+#pragma unroll
+            for (int t = 0; t < TILES; t++) {
+                const int tok = 16 * (wt * TILES + t) + n;
+                bx[t] = *(const h8_t *)&sx[st][j][tok][8 * q];
+                yd[t] = sxd[st][j][tok];
+            }
+#pragma unroll
+            for (int s = 0; s < SETS; s++) {
+                const int r0 = 4 * (wr * SETS + s);  // first row of the set in the block
+                const _Float16 *ap = a_on ? &sw[st][r0 + a_row][j][8 * q] : szero;
+                const h4_t lo = *(const h4_t *)ap, hi = *(const h4_t *)(ap + 4);
+                const _Float16 z = (_Float16)0;
+                const h8_t ae = {lo[0], lo[1], lo[2], lo[3], z, z, z, z};
+                const h8_t ao = {z, z, z, z, hi[0], hi[1], hi[2], hi[3]};
+                const float dw = swd[st][r0 + q][j];
+#pragma unroll
+                for (int t = 0; t < TILES; t++) {  // (tiles past the batch compute on repeated tokens)
+                    const f4_t pe = __builtin_amdgcn_mfma_f32_16x16x32_f16(ae, bx[t], f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    const f4_t po = __builtin_amdgcn_mfma_f32_16x16x32_f16(ao, bx[t], f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    const float D = dw * yd[t];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        acc[s][t][0][i] = fmaf(D, pe[i], acc[s][t][0][i]);
+                        acc[s][t][1][i] = fmaf(D, po[i], acc[s][t][1][i]);
                     }
                 }
             }
-            *(u32x4_t *)&sw[st][wr_row][wr_blk][0] = lo;
-            *(u32x4_t *)&sw[st][wr_row][wr_blk][16] = hi;
-            swd[st][wr_row][wr_blk] = f16_to_f32(lwd);
+        }
+        if (c0 + MQ_BS < nb) {
+            put(pr, st ^ 1);
+            __syncthreads();
         }
     };
-    float acc[R][8];
+    for (int c0 = 0; c0 < nb; c0 += 2 * MQ_BS) {
+        round(c0, 0, L[0], L[1]);
+        if (c0 + MQ_BS < nb) round(c0 + MQ_BS, 1, L[1], L[0]);
+    }
+    // lane (q, n): row r0 + q of each set, token 16 * tile + n; groups 2i (even) and 2i + 1 (odd)
 #pragma unroll
-    for (int r = 0; r < R; r++)
+    for (int s = 0; s < SETS; s++) {
+        const int grow = row0 + 4 * (wr * SETS + s) + q;
 #pragma unroll
-        for (int l = 0; l < 8; l++) acc[r][l] = 0.0f;
-    fetch(0);
-    put(0);
-    __syncthreads();
-    int st = 0;
-    for (int c0 = 0; c0 < nb; c0 += MQ_BS) {
-        const bool more = c0 + MQ_BS < nb;
-        if (more) fetch(c0 + MQ_BS);
-        const int n = nb - c0 < MQ_BS ? nb - c0 : MQ_BS;
-        for (int j = 0; j < n; j++) {
-            const u32x4_t y0 = *(const u32x4_t *)&sx[st][j][lane][0], y1 = *(const u32x4_t *)&sx[st][j][lane][16];
-            const float yd = sxd[st][j][lane];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                // the same address in every lane: LDS broadcasts
-                const u32x4_t w0 = *(const u32x4_t *)&sw[st][R * wave + r][j][0];
-                const u32x4_t w1 = *(const u32x4_t *)&sw[st][R * wave + r][j][16];
-                const float D = swd[st][R * wave + r][j] * yd;
-#pragma unroll
-                for (int l = 0; l < 4; l++) {
-                    acc[r][l] = fmaf(D, (float)dot4(w0[l], y0[l], 0), acc[r][l]);
-                    acc[r][l + 4] = fmaf(D, (float)dot4(w1[l], y1[l], 0), acc[r][l + 4]);
-                }
-            }
-        }
-        if (more) {
-            put(st ^ 1);  // last read in the previous round, before its barrier
-            __syncthreads();
-            st ^= 1;
+        for (int t = 0; t < TILES; t++) {
+            const int tt = 16 * (wt * TILES + t) + n;
+            const f4_t e = acc[s][t][0], o = acc[s][t][1];
+            // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7))  (simd_avx2.rs:27-34), a_{2i} = e[i], a_{2i+1} = o[i]
+            const float v = ((e[0] + e[2]) + (e[1] + e[3])) + ((o[0] + o[2]) + (o[1] + o[3]));
+            if (tt < mt && grow < a.total_rows) store_row(a, grow, t0 + tt, v);
         }
     }
-    const int tok = t0 + lane;
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const int grow = row0 + R * wave + r;
-        if (tok < m && grow < a.total_rows) store_row(a, grow, tok, hsum8(acc[r]));
+}
+
+template <int KIND>
+static void launch_mm_q8(const MvArgs &a, int m, hipStream_t s) {
+    // the quants as f16 once per batch
+    const size_t n16 = (size_t)m * a.cols / 16;
+    k_q8_to_f16<<<(unsigned)((n16 + 255) / 256), 256, 0, s>>>(a.xq, a.xh, n16);
+    // rows per block by the matrix height: enough waves for few rows, more
+    // reuse of each staged activation for many
+    const unsigned gy = (unsigned)((m + 63) / 64);
+    if (a.total_rows >= 16384) {
+        k_mm_q8<KIND, 2, 4><<<dim3((unsigned)((a.total_rows + 31) / 32), gy), 256, 0, s>>>(a, m);
+    } else if (a.total_rows >= 6144) {
+        k_mm_q8<KIND, 2, 2><<<dim3((unsigned)((a.total_rows + 15) / 16), gy), 256, 0, s>>>(a, m);
+    } else {
+        k_mm_q8<KIND, 2, 1><<<dim3((unsigned)((a.total_rows + 7) / 8), gy), 256, 0, s>>>(a, m);
     }
 }
 
@@ -1789,6 +1888,7 @@ static MvArgs make_args(int n, const DevWeight *const ws[], float *const ys[], c
         ActQ8_0 q = *(const ActQ8_0 *)x_act;
         a.xq = q.qs;
         a.xd = q.d;
+        a.xh = q.xh;
     } else {
         a.xf = (const float *)x_act;
     }
@@ -1899,14 +1999,13 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
 #undef MMK
         return;
     }
-    if (m >= MM_MIN_TOKENS && (kind == AOTK_Q8_0 || kind == AOTK_Q4_0 || kind == AOTK_Q5_0 ||
+    if (m >= MM_MIN_TOKENS && (((kind == AOTK_Q8_0 || kind == AOTK_Q4_0 || kind == AOTK_Q5_0) && a.xh) ||
                                ((kind == AOTK_F16 || kind == AOTK_BF16 || kind == AOTK_F32) && mm_float_fits(a, kind)))) {
         dim3 g((unsigned)((a.total_rows + 4 * MQ_R - 1) / (4 * MQ_R)), (unsigned)((m + 63) / 64));
-        // (k_mm_float keeps the same rows per block)
         switch (kind) {
-        case AOTK_Q8_0: k_mm_q8<AOTK_Q8_0><<<g, 256, 0, s>>>(a, (int)m); break;
-        case AOTK_Q4_0: k_mm_q8<AOTK_Q4_0><<<g, 256, 0, s>>>(a, (int)m); break;
-        case AOTK_Q5_0: k_mm_q8<AOTK_Q5_0><<<g, 256, 0, s>>>(a, (int)m); break;
+        case AOTK_Q8_0: launch_mm_q8<AOTK_Q8_0>(a, (int)m, s); break;
+        case AOTK_Q4_0: launch_mm_q8<AOTK_Q4_0>(a, (int)m, s); break;
+        case AOTK_Q5_0: launch_mm_q8<AOTK_Q5_0>(a, (int)m, s); break;
         case AOTK_F16: k_mm_float<AOTK_F16><<<g, 256, 0, s>>>(a, (int)m); break;
         case AOTK_BF16: k_mm_float<AOTK_BF16><<<g, 256, 0, s>>>(a, (int)m); break;
         default: k_mm_float<AOTK_F32><<<g, 256, 0, s>>>(a, (int)m); break;

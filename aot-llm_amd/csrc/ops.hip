@@ -123,6 +123,7 @@ __device__ __forceinline__ ActQ8_0 q80_row(ActQ8_0 a, size_t row, size_t n) {
     ActQ8_0 r = a;
     r.qs += row * n;
     r.d += row * (n / 32);
+    if (r.xh) r.xh += row * n;
     return r;
 }
 
