@@ -731,7 +731,7 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     if (tid < DB) a.out[i * (size_t)a.n_head * HD + (size_t)h * HD + d0 + tid] = o;
 }
 
-// Batched rows (prompt chunks), spans up to ATT_ROWS_MAX: the same softmax
+// Batched rows (prompt chunks), spans up to ATT_MAX_SPAN: the same softmax
 // and output, with the serial chains spread over lanes instead of blocks.
 //   k_attn_softmax_rows: one wave per (row, head): max, glibc-matched exp
 //   into LDS, the sequential sum by lane 0, then p = e * (1 / sum) written
@@ -740,13 +740,14 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
 //   keeps the ATT_RB sums of dim d and adds p_t * v_t,d in position order;
 //   V rows are read straight from the cache (256 B per wave per position),
 //   the probabilities with wave-uniform loads.
-constexpr int ATT_ROWS_MAX = 2048;
+constexpr int ATT_ROWS_MAX = 2048;  // spans of the 4-wave softmax blocks (one wave per block up to ATT_MAX_SPAN)
 constexpr int ATT_RB = 4;
 
-__global__ __launch_bounds__(256) void k_attn_softmax_rows(AttnArgs a, int m) {
-    __shared__ __align__(16) float e[4][ATT_ROWS_MAX];
+template <int NW, int CAP>
+__global__ __launch_bounds__(64 * NW) void k_attn_softmax_rows(AttnArgs a, int m) {
+    __shared__ __align__(16) float e[NW][CAP];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int pair = blockIdx.x * 4 + w;
+    const int pair = blockIdx.x * NW + w;
     if (pair >= m * a.n_head) return;
     const int i = pair / a.n_head, h = pair % a.n_head;
     size_t t0, n;
@@ -863,9 +864,11 @@ __global__ __launch_bounds__(256) void k_attn_out_rows(AttnArgs a, int m) {
         if (rg * ATT_RB + r < m) a.out[(size_t)row[r] * a.n_head * HD + (size_t)h * HD + d] = o[r];
 }
 
-static void launch_rows(const AttnArgs &a, size_t head_dim, size_t m, hipStream_t s) {
+static void launch_rows(const AttnArgs &a, size_t head_dim, size_t m, size_t longest, hipStream_t s) {
     const unsigned pairs = (unsigned)(m * a.n_head);
-    k_attn_softmax_rows<<<(pairs + 3) / 4, 256, 0, s>>>(a, (int)m);
+    if (longest <= (size_t)ATT_ROWS_MAX) k_attn_softmax_rows<4, ATT_ROWS_MAX><<<(pairs + 3) / 4, 256, 0, s>>>(a, (int)m);
+    else if (longest <= 8192) k_attn_softmax_rows<1, 8192><<<pairs, 64, 0, s>>>(a, (int)m);
+    else k_attn_softmax_rows<1, ATT_MAX_SPAN><<<pairs, 64, 0, s>>>(a, (int)m);
     const size_t tasks = (m + ATT_RB - 1) / ATT_RB * a.n_head * (head_dim / 64);
     const unsigned g = (unsigned)((tasks + 3) / 4);
     switch (head_dim) {
@@ -933,8 +936,8 @@ void launch_attention(float *out, const float *q, const float *k_cache, const fl
     }
     // the longest row spans min(pos0 + m, window) positions
     const size_t longest = window > 0 && window < pos0 + m ? window : pos0 + m;
-    if (m > 1 && !pos_dev && longest <= (size_t)ATT_ROWS_MAX)
-        launch_rows(a, head_dim, m, s);
+    if (m > 1 && !pos_dev && longest <= (size_t)ATT_MAX_SPAN)
+        launch_rows(a, head_dim, m, longest, s);
     else
         launch_sv(a, head_dim, m, s);
 }

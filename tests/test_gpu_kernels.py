@@ -265,9 +265,9 @@ def test_attention(aotk, oracle, hd, nh, nkv, window):
 
 
 @pytest.mark.parametrize("hd,nh,nkv,window,ctx,cases", [
-    (128, 32, 8, 0, 4400, ((4300, 1), (2100, 2), (1500, 1), (1980, 64))),
+    (128, 32, 8, 0, 4400, ((4300, 1), (2100, 2), (1500, 1), (1980, 64), (4000, 64))),
     (256, 8, 4, 1024, 8300, ((8200, 1), (700, 3), (1000, 40))),
-    (256, 8, 4, 0, 8300, ((8200, 1), (5000, 2))),
+    (256, 8, 4, 0, 8300, ((8200, 1), (5000, 2), (8100, 64))),
 ])
 def test_attention_long_spans(aotk, oracle, hd, nh, nkv, window, ctx, cases):
     """Spans past the one-thread softmax sum (exact parallel replay) and past
