@@ -102,12 +102,19 @@ __device__ __forceinline__ float seq_sum_lds_pad64(const float *v, int n) {
     return s;
 }
 
-// ss = sum of v*v over n values in LDS, in index order (ops.rs:10-13). Run
-// by one thread; the result is broadcast through LDS.
-__device__ float seq_sumsq_lds(const float *v, int n, float *bcast) {
-    if (threadIdx.x == 0) *bcast = seq_sum_lds<true>(v, n);
-    __syncthreads();
-    return *bcast;
+// ss = sum of v*v over n <= 256 values in LDS, in index order
+// (ops.rs:10-13), for one wave: the lanes form the squares (each rounded as
+// in the sequential loop) into tmp, padded with -0.0 to a run of 64 (neutral
+// under round to nearest), then lane 0 adds them in order with the LDS
+// chain; the result is returned to every lane.
+__device__ __forceinline__ float wave_sumsq_lds(const float *v, float *tmp, int n) {
+    const int lane = threadIdx.x & 63;
+    const int n64 = (n + 63) & ~63;
+    for (int e = lane; e < n64; e += 64) tmp[e] = e < n ? v[e] * v[e] : -0.0f;
+    wave_lds_sync();
+    float ss = 0.0f;
+    if (lane == 0) ss = seq_sum_lds_pad64(tmp, n);
+    return __shfl(ss, 0, 64);
 }
 
 __device__ __forceinline__ ActQ8K q8k_row(ActQ8K a, size_t row, size_t n) {
@@ -277,8 +284,8 @@ __global__ __launch_bounds__(64) void k_qkv_post(QkvPost p, size_t pos0, const i
     }
     __syncthreads();
     if (nw) {
-        __shared__ float bc;
-        float ss = seq_sumsq_lds(hv, hd, &bc);
+        __shared__ __align__(16) float sqt[256];
+        float ss = wave_sumsq_lds(hv, sqt, hd);
         float r = 1.0f / sqrtf(ss / (float)hd + p.eps);
         for (int e = lane; e < hd; e += 64) hv[e] = hv[e] * r * nw[e];
         __syncthreads();
@@ -455,33 +462,75 @@ __global__ __launch_bounds__(512) void k_attn_scores_rb(AttnArgs a, int m) {
 
 // One wave's share of the q/k/v epilogue for one head vector (decode):
 // bias, rmsnorm_heads (sequential sum of squares by lane 0), rope with the
-// position's table row; the result is left in `hv` (LDS, hd floats).
-__device__ __forceinline__ void head_post_wave(float *hv, const float *src, const float *bias, const float *nw,
-                                               const float *cs_row, int hd, int rot_dim, int neox, float eps) {
+// position's table row; the result is left in `hv` (LDS, HD floats). The
+// inputs (the vector, its bias, the norm weights, the rope row) are loaded
+// by head_load first, so that loads the caller issues afterwards (the K rows
+// of the chunk) do not delay them.
+template <int HD>
+struct HeadIn {
+    static constexpr int NE = (HD + 63) / 64;
+    float v[NE], bv[NE], wv[NE];
+    float2 cs[NE];
+};
+template <int HD>
+__device__ __forceinline__ void head_load(HeadIn<HD> &in, const float *src, const float *bias, const float *nw,
+                                          const float *cs_row, int rot_dim) {
+    // unconditional loads (absent inputs read the vector itself, indices
+    // past the end repeat the last element): no branch, so no wait, between
+    // them
     const int lane = threadIdx.x & 63;
-    for (int e = lane; e < hd; e += 64) {
-        float v = src[e];
-        if (bias) v = v + bias[e];
-        hv[e] = v;
+    const int half = rot_dim / 2;
+    const float *bp = bias ? bias : src, *wp = nw ? nw : src;
+    const float2 *cp = (const float2 *)cs_row;
+#pragma unroll
+    for (int k = 0; k < HeadIn<HD>::NE; k++) {
+        const int e = min(lane + 64 * k, HD - 1);
+        in.v[k] = src[e];
+        in.bv[k] = bp[e];
+        in.wv[k] = wp[e];
+        in.cs[k] = cp[max(min(lane + 64 * k, half - 1), 0)];  // (rot_dim > 0 on this path)
+    }
+}
+#ifndef EPI_TS
+#define EPI_TS(i)
+#endif
+template <int HD>
+__device__ __forceinline__ void head_post_wave(float *hv, float *tmp, const HeadIn<HD> &in, bool bias, bool norm,
+                                               int rot_dim, int neox, float eps) {
+    constexpr int NE = HeadIn<HD>::NE;
+    const int lane = threadIdx.x & 63;
+    const int half = rot_dim / 2;
+#pragma unroll
+    for (int k = 0; k < NE; k++) {
+        const int e = lane + 64 * k;
+        if (e < HD) hv[e] = bias ? in.v[k] + in.bv[k] : in.v[k];
     }
     wave_lds_sync();
-    if (nw) {
-        float ss = 0.0f;
-        if (lane == 0) ss = seq_sum_lds<true>(hv, hd);
-        ss = __shfl(ss, 0, 64);
-        const float r = 1.0f / sqrtf(ss / (float)hd + eps);
-        for (int e = lane; e < hd; e += 64) hv[e] = hv[e] * r * nw[e];
+    EPI_TS(4);
+    if (norm) {
+        const float ss = wave_sumsq_lds(hv, tmp, HD);
+        EPI_TS(5);
+        const float r = 1.0f / sqrtf(ss / (float)HD + eps);
+#pragma unroll
+        for (int k = 0; k < NE; k++) {
+            const int e = lane + 64 * k;
+            if (e < HD) hv[e] = hv[e] * r * in.wv[k];
+        }
         wave_lds_sync();
     }
-    const int half = rot_dim / 2;
-    for (int t = lane; t < half; t += 64) {
-        const float c = cs_row[2 * t], sn = cs_row[2 * t + 1];
-        const int ia = neox ? t : 2 * t, ib = neox ? t + half : 2 * t + 1;
-        const float x0 = hv[ia], x1 = hv[ib];
-        hv[ia] = x0 * c - x1 * sn;
-        hv[ib] = x0 * sn + x1 * c;
+#pragma unroll
+    for (int k = 0; k < NE; k++) {
+        const int t = lane + 64 * k;
+        if (t < half) {
+            const float c = in.cs[k].x, sn = in.cs[k].y;
+            const int ia = neox ? t : 2 * t, ib = neox ? t + half : 2 * t + 1;
+            const float x0 = hv[ia], x1 = hv[ib];
+            hv[ia] = x0 * c - x1 * sn;
+            hv[ib] = x0 * sn + x1 * c;
+        }
     }
     wave_lds_sync();
+    EPI_TS(6);
 }
 
 // Decode (one row) scores with the q/k/v epilogue fused in: block = (kv head,
@@ -491,11 +540,18 @@ __device__ __forceinline__ void head_post_wave(float *hv, const float *src, cons
 // cache. The chunk's K rows are staged in LDS (the new position's row from
 // the post-processed k), then thread (query head, position) runs its dot
 // product sequentially over the head dimension.
+#ifndef QK_TS
+#define QK_TS(i)
+#endif
+// (head_dim 256: at most 4 query heads per kv head, so that the block's
+// 22 float4 of K per thread stay in registers)
+constexpr int QKD_MAX_GQA_256 = 4;
 template <int HD>
-__global__ __launch_bounds__(576) void k_attn_qk_decode(AttnArgs a, QkvPost p) {
+__global__ __launch_bounds__(HD == 256 ? 64 * (QKD_MAX_GQA_256 + 1) : 576) void k_attn_qk_decode(AttnArgs a, QkvPost p) {
     constexpr int KS = HD + 1;
     __shared__ float sk[ATT_CH * KS];
     __shared__ __align__(16) float sq[ATT_MAX_GQA + 1][HD];
+    __shared__ __align__(16) float ssq[ATT_MAX_GQA + 1][HD];  // squares for the q/k norms
     const int gqa = a.n_head / a.n_kv_head;
     const int lane = threadIdx.x & 63, hg = threadIdx.x >> 6;
     const int kvh = blockIdx.x, c = blockIdx.y;
@@ -507,12 +563,25 @@ __global__ __launch_bounds__(576) void k_attn_qk_decode(AttnArgs a, QkvPost p) {
     const int rows = (int)min((size_t)ATT_CH, n - start);
     const size_t kv = (size_t)a.n_kv_head * HD;
     const float *cs_row = p.cs + pos * p.rot_dim;
-    // the chunk's K rows do not depend on the epilogue: the first PK float4
-    // of each thread are loaded before it (the new position's row is filled
-    // from the post-processed k below)
+    QK_TS(0);
+    // the epilogue's inputs first, then the chunk's K rows, which do not
+    // depend on it: the first PK float4 of each thread are in flight during
+    // the epilogue (the new position's row is filled from the post-processed
+    // k below)
+    HeadIn<HD> hin;
+    if (hg < gqa) {
+        const int h = kvh * gqa + hg;
+        head_load<HD>(hin, p.q + (size_t)h * HD, p.bq ? p.bq + (size_t)h * HD : nullptr, p.q_norm, cs_row, (int)p.rot_dim);
+    } else {
+        head_load<HD>(hin, p.k + (size_t)kvh * HD, p.bk ? p.bk + (size_t)kvh * HD : nullptr, p.k_norm, cs_row,
+                      (int)p.rot_dim);
+    }
     const float *kb = a.k_cache + start * kv + (size_t)kvh * HD;
     constexpr int R4 = HD / 4;
-    constexpr int PK = 8;
+    // every float4 of the chunk a thread loads is in flight at once: up to
+    // ATT_CH * HD / 4 over (gqa + 1) * 64 >= 192 threads (gqa >= 2 for
+    // HD 256; smaller groups take the loop below for the rest)
+    constexpr int PK = HD == 256 ? 22 : 8;
     const int nthreads = (gqa + 1) * 64;
     float4 kpre[PK];
 #pragma unroll
@@ -523,13 +592,10 @@ __global__ __launch_bounds__(576) void k_attn_qk_decode(AttnArgs a, QkvPost p) {
                                                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     if (hg < gqa) {
-        const int h = kvh * gqa + hg;
-        head_post_wave(sq[hg], p.q + (size_t)h * HD, p.bq ? p.bq + (size_t)h * HD : nullptr, p.q_norm, cs_row, HD,
-                       (int)p.rot_dim, p.neox, p.eps);
+        head_post_wave<HD>(sq[hg], ssq[hg], hin, p.bq != nullptr, p.q_norm != nullptr, (int)p.rot_dim, p.neox, p.eps);
     } else {
         float *kn = sq[ATT_MAX_GQA];
-        head_post_wave(kn, p.k + (size_t)kvh * HD, p.bk ? p.bk + (size_t)kvh * HD : nullptr, p.k_norm, cs_row, HD,
-                       (int)p.rot_dim, p.neox, p.eps);
+        head_post_wave<HD>(kn, ssq[ATT_MAX_GQA], hin, p.bk != nullptr, p.k_norm != nullptr, (int)p.rot_dim, p.neox, p.eps);
         if (pos >= start && pos < start + ATT_CH) {
             float *kc = p.k_cache + pos * kv + (size_t)kvh * HD;
             float *vc = p.v_cache + pos * kv + (size_t)kvh * HD;
@@ -541,6 +607,7 @@ __global__ __launch_bounds__(576) void k_attn_qk_decode(AttnArgs a, QkvPost p) {
             }
         }
     }
+    QK_TS(1);
     // K rows of the chunk into LDS (the new position from the post-processed k)
 #pragma unroll
     for (int j = 0; j < PK; j++) {
@@ -571,6 +638,7 @@ __global__ __launch_bounds__(576) void k_attn_qk_decode(AttnArgs a, QkvPost p) {
         for (int e = threadIdx.x; e < HD; e += nthreads) sk[r * KS + e] = sq[ATT_MAX_GQA][e];
         __syncthreads();
     }
+    QK_TS(2);
     if (hg >= gqa || lane >= rows) return;
     const float *kr = sk + lane * KS;
     const float *qq = sq[hg];
@@ -578,6 +646,7 @@ __global__ __launch_bounds__(576) void k_attn_qk_decode(AttnArgs a, QkvPost p) {
 #pragma unroll 16
     for (int d = 0; d < HD; d++) sc += qq[d] * kr[d];
     a.prob[(size_t)(kvh * gqa + hg) * a.span + (start + lane - t0)] = sc * a.scale;
+    QK_TS(3);
 }
 
 // Softmax and output per (row, head, group of SV_DB dims): block of SEQ_T

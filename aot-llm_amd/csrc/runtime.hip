@@ -522,6 +522,7 @@ static int validate_spec(const aotk_model_spec *s, size_t blob_len) {
                                                                  (unsigned long long)d.n_head, (unsigned long long)d.n_kv_head);
     if (d.n_head / d.n_kv_head > 8) return fail("spec: gqa > 8 unsupported");
     if (d.head_dim != 64 && d.head_dim != 128 && d.head_dim != 256) return fail("spec: head_dim %llu unsupported", (unsigned long long)d.head_dim);
+    if (d.head_dim == 256 && d.n_head / d.n_kv_head > 4) return fail("spec: head_dim 256 supports at most 4 query heads per kv head");
     if (d.rot_dim > d.head_dim || d.rot_dim % 2) return fail("spec: bad rot_dim");
     size_t qd = d.n_head * d.head_dim;
     if (d.dim % 256 || d.hidden % 256 || qd % 256 || d.dim > 8192)
