@@ -551,7 +551,6 @@ __global__ __launch_bounds__(HD == 256 ? 64 * (QKD_MAX_GQA_256 + 1) : 576) void 
     constexpr int KS = HD + 1;
     __shared__ float sk[ATT_CH * KS];
     __shared__ __align__(16) float sq[ATT_MAX_GQA + 1][HD];
-    __shared__ __align__(16) float ssq[ATT_MAX_GQA + 1][HD];  // squares for the q/k norms
     const int gqa = a.n_head / a.n_kv_head;
     const int lane = threadIdx.x & 63, hg = threadIdx.x >> 6;
     const int kvh = blockIdx.x, c = blockIdx.y;
@@ -592,10 +591,10 @@ __global__ __launch_bounds__(HD == 256 ? 64 * (QKD_MAX_GQA_256 + 1) : 576) void 
                                                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     if (hg < gqa) {
-        head_post_wave<HD>(sq[hg], ssq[hg], hin, p.bq != nullptr, p.q_norm != nullptr, (int)p.rot_dim, p.neox, p.eps);
+        head_post_wave<HD>(sq[hg], sk + hg * HD, hin, p.bq != nullptr, p.q_norm != nullptr, (int)p.rot_dim, p.neox, p.eps);
     } else {
         float *kn = sq[ATT_MAX_GQA];
-        head_post_wave<HD>(kn, ssq[ATT_MAX_GQA], hin, p.bk != nullptr, p.k_norm != nullptr, (int)p.rot_dim, p.neox, p.eps);
+        head_post_wave<HD>(kn, sk + gqa * HD, hin, p.bk != nullptr, p.k_norm != nullptr, (int)p.rot_dim, p.neox, p.eps);
         if (pos >= start && pos < start + ATT_CH) {
             float *kc = p.k_cache + pos * kv + (size_t)kvh * HD;
             float *vc = p.v_cache + pos * kv + (size_t)kvh * HD;
@@ -608,6 +607,7 @@ __global__ __launch_bounds__(HD == 256 ? 64 * (QKD_MAX_GQA_256 + 1) : 576) void 
         }
     }
     QK_TS(1);
+    __syncthreads();  // the epilogue used sk for the squares of the norms
     // K rows of the chunk into LDS (the new position from the post-processed k)
 #pragma unroll
     for (int j = 0; j < PK; j++) {
