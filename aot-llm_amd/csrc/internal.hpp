@@ -205,6 +205,9 @@ void launch_attention_decode(float *out, const QkvPost &p, size_t ctx_rows, size
                              const int *pos_dev, float *scratch, hipStream_t s);
 void launch_add(float *x, const float *y, size_t n, hipStream_t s);
 void launch_rmsnorm_add(float *x, const float *y, const float *w, size_t n, size_t m, float eps, hipStream_t s);
+// x += rmsnorm(y) * w_post, then rmsnorm(x) * w_next quantized into `out`.
+void launch_rmsnorm_add_quant(float *x, const float *y, const float *w_post, const float *w_next, size_t n, size_t m,
+                              float eps, RmsOut out, hipStream_t s);
 void launch_argmax(const float *x, size_t n, uint32_t *out_dev, float *scratch, hipStream_t s);
 void launch_advance(uint32_t *tok_dev, int *counter_dev, uint32_t *hist, const uint32_t *argmax_dev, hipStream_t s);
 void launch_inc(int *p, hipStream_t s);

@@ -1073,6 +1073,78 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_add(float *x, const float *y,
         if (i < n) xr[i] = xv[k] + yv[k] * r * wv[k];
     }
 }
+// Gemma: the post-norm join x += rmsnorm(y) (emit.rs:320-324) and the next
+// rmsnorm of x with its quantization (the following block's input), in one
+// launch: the updated row stays in registers between the two exact sums.
+__global__ __launch_bounds__(SEQ_T) void k_rmsnorm_add_quant(float *x, const float *y, const float *w_post,
+                                                             const float *w_next, int n, float eps, RmsOut out) {
+    __shared__ __align__(16) float row[8192];
+    __shared__ float sq[SEQ_PAD_N];
+    __shared__ SeqScratch S;
+    const size_t m = blockIdx.x;
+    const float *yr = y + m * n;
+    float *xr = x + m * n;
+    const int C = seq_chunk(n);
+    float yv[8], xv[8], wv[8], wn[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) yv[k] = yr[min((int)threadIdx.x + k * SEQ_T, n - 1)];
+#pragma unroll
+    for (int k = 0; k < 8; k++) xv[k] = xr[min((int)threadIdx.x + k * SEQ_T, n - 1)];
+#pragma unroll
+    for (int k = 0; k < 8; k++) wv[k] = w_post[min((int)threadIdx.x + k * SEQ_T, n - 1)];
+#pragma unroll
+    for (int k = 0; k < 8; k++) wn[k] = w_next[min((int)threadIdx.x + k * SEQ_T, n - 1)];
+#pragma unroll
+    for (int k = 0; k < 8; k++) asm volatile("" : "+v"(yv[k]));
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i = threadIdx.x + k * SEQ_T;
+        if (i < n) sq[seq_idx(i, C)] = yv[k] * yv[k];
+    }
+    __syncthreads();
+    const float ss = exact_seq_sum(sq, n, S);
+    const float r = 1.0f / sqrtf(ss / (float)n + eps);
+    // x += y * r * w (as k_rmsnorm_add), then the squares of the new x
+    // (exact_seq_sum's closing barrier orders these writes after its reads)
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i = threadIdx.x + k * SEQ_T;
+        if (i < n) {
+            const float v = xv[k] + yv[k] * r * wv[k];
+            xv[k] = v;
+            xr[i] = v;
+            row[i] = v;
+            sq[seq_idx(i, C)] = v * v;
+        }
+    }
+    __syncthreads();
+    const float ss2 = exact_seq_sum(sq, n, S);
+    const float r2 = 1.0f / sqrtf(ss2 / (float)n + eps);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int i = threadIdx.x + k * SEQ_T;
+        if (i < n) {
+            const float v = row[i] * r2 * wn[k];
+            row[i] = v;
+            if (out.f32) out.f32[m * n + i] = v;
+        }
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    ActQ8K qk = q8k_row(out.q8k, m, n);
+    ActQ8_0 q0 = q80_row(out.q80, m, n);
+    for (int b = wave; b < n / 256; b += nw) {
+        float4 v4 = ((const float4 *)(row + b * 256))[lane];
+        float v[4] = {v4.x, v4.y, v4.z, v4.w};
+        quant256(v, lane, b, qk, q0);
+    }
+}
+
+void launch_rmsnorm_add_quant(float *x, const float *y, const float *w_post, const float *w_next, size_t n, size_t m,
+                              float eps, RmsOut out, hipStream_t s) {
+    k_rmsnorm_add_quant<<<(unsigned)m, SEQ_T, 0, s>>>(x, y, w_post, w_next, (int)n, eps, out);
+}
+
 void launch_rmsnorm_add(float *x, const float *y, const float *w, size_t n, size_t m, float eps, hipStream_t s) {
     k_rmsnorm_add<<<(unsigned)m, SEQ_T, 0, s>>>(x, y, w, (int)n, eps);
 }

@@ -1002,12 +1002,15 @@ static void run_layers(aotk_state *st, size_t m, size_t pos0, const int *pos_dev
     const aotk_flags &f = M->spec.flags;
     hipStream_t s = g_stream;
     size_t dim = d.dim, qd = d.n_head * d.head_dim, kv = d.n_kv_head * d.head_dim;
+    bool normed = false;  // this layer's attention norm done by the previous layer's post-norm join
     for (size_t l = 0; l < d.n_layer; l++) {
         LayerDev &L = M->dev[l];
         float *kc = st->k_cache + l * st->ctx * kv;
         float *vc = st->v_cache + l * st->ctx * kv;
         // attention block
-        launch_rmsnorm_quant(st->x, L.attn_norm, dim, m, d.eps, outs_for(st, {L.wq.kind, L.wk.kind, L.wv.kind}, st->xb), s);
+        if (!normed)
+            launch_rmsnorm_quant(st->x, L.attn_norm, dim, m, d.eps, outs_for(st, {L.wq.kind, L.wk.kind, L.wv.kind}, st->xb), s);
+        normed = false;
         bool same = L.wq.kind == L.wk.kind && L.wk.kind == L.wv.kind && activation(L.wq.kind) != ACT_F32;
         if (same) {
             const DevWeight *ws[3] = {&L.wq, &L.wk, &L.wv};
@@ -1055,9 +1058,12 @@ static void run_layers(aotk_state *st, size_t m, size_t pos0, const int *pos_dev
             if (activation(L.wo.kind) != ACT_F32) launch_quant_f32(st->xb, qd, m, outs_for(st, {L.wo.kind}, nullptr), s);
             launch_matvec(L.wo, act_for(st, L.wo.kind, st->xb), m, wo_y, wo_add, s);
         }
-        if (f.post_norms) launch_rmsnorm_add(st->x, st->xb2, L.attn_post_norm, dim, m, d.eps, s);
-        // feed-forward block
-        launch_rmsnorm_quant(st->x, L.ffn_norm, dim, m, d.eps, outs_for(st, {L.gate.kind, L.up.kind}, st->xb), s);
+        // feed-forward block (Gemma: the post-norm join and the ffn norm in one launch)
+        if (f.post_norms)
+            launch_rmsnorm_add_quant(st->x, st->xb2, L.attn_post_norm, L.ffn_norm, dim, m, d.eps,
+                                     outs_for(st, {L.gate.kind, L.up.kind}, st->xb), s);
+        else
+            launch_rmsnorm_quant(st->x, L.ffn_norm, dim, m, d.eps, outs_for(st, {L.gate.kind, L.up.kind}, st->xb), s);
         bool same2 = L.gate.kind == L.up.kind && activation(L.gate.kind) != ACT_F32;
         if (same2) {
             const DevWeight *ws[2] = {&L.gate, &L.up};
@@ -1070,7 +1076,14 @@ static void run_layers(aotk_state *st, size_t m, size_t pos0, const int *pos_dev
         launch_glu_quant(st->hb, st->hb2, d.hidden, m, f.gelu, outs_for(st, {L.down.kind}, st->hb), s);
         if (f.post_norms) {
             launch_matvec(L.down, act_for(st, L.down.kind, st->hb), m, st->xb2, nullptr, s);
-            launch_rmsnorm_add(st->x, st->xb2, L.ffn_post_norm, dim, m, d.eps, s);
+            if (l + 1 < d.n_layer) {  // the join and the next layer's attention norm in one launch
+                const LayerDev &N = M->dev[l + 1];
+                launch_rmsnorm_add_quant(st->x, st->xb2, L.ffn_post_norm, N.attn_norm, dim, m, d.eps,
+                                         outs_for(st, {N.wq.kind, N.wk.kind, N.wv.kind}, st->xb), s);
+                normed = true;
+            } else {
+                launch_rmsnorm_add(st->x, st->xb2, L.ffn_post_norm, dim, m, d.eps, s);
+            }
         } else {
             launch_matvec(L.down, act_for(st, L.down.kind, st->hb), m, st->x, st->x, s);
         }
