@@ -391,7 +391,8 @@ __global__ void k_quant_q8_0(const float *__restrict__ x, size_t nblk, ActQ8_0 o
     size_t blk = i / 32;
     if (blk >= nblk) return;
     float v = x[i];
-    float amax = fabsf(v);
+    // fold(0, max) of |v| (quant.rs:237): NaN never wins, an all-NaN block gives 0
+    float amax = fmaxf(0.0f, fabsf(v));
     for (int m = 1; m < 32; m <<= 1) amax = fmaxf(amax, shfl_xor(amax, m));
     float d = amax / 127.0f;
     float id = d != 0.0f ? 1.0f / d : 0.0f;

@@ -62,6 +62,10 @@ def test_activation_quantizers(aotk, oracle):
         a0 = aotk.quantize_q8_0(x)
         b0 = oracle.quantize_q8_0(x)
         assert a0.tobytes() == b0.tobytes()
+        xn = x.copy()
+        xn[64:96] = np.nan  # an all-NaN block: fold(0, max) gives d = 0
+        xn[100] = np.nan    # and a NaN among finite values never wins the max
+        assert aotk.quantize_q8_0(xn).tobytes() == oracle.quantize_q8_0(xn).tobytes()
 
 
 @pytest.mark.parametrize("kind", ALL, ids=lambda k: NAMES[k])
