@@ -671,12 +671,12 @@ constexpr int SV_DB = 32;         // dims per block
 constexpr int SV_CP = 192;        // positions per chunk
 constexpr int SV_RS = SV_CP + 4;  // floats per dim row of the product buffer
 constexpr int SV_BUF = SV_DB * SV_RS;  // floats per product buffer
-constexpr int SV_SEQ_MIN = 2048;  // shorter spans are summed by one thread
+constexpr int SV_SEQ_MIN = 512;  // shorter spans are summed by one thread
 template <int HD>
 __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     constexpr int DB = SV_DB;
     constexpr int CP = SV_CP;
-    __shared__ __align__(16) float e[ATT_MAX_SPAN + 64];
+    __shared__ __align__(16) float e[SEQ_PAD_N > ATT_MAX_SPAN + 64 ? SEQ_PAD_N : ATT_MAX_SPAN + 64];
     // product buffers (+64 floats read past the end by the last groups) / sum scratch
     __shared__ __align__(16) uint8_t ubuf[sizeof(SeqScratch) > (2 * SV_BUF + 64) * 4 ? sizeof(SeqScratch) : (2 * SV_BUF + 64) * 4];
     __shared__ float red[SEQ_T / 64];
