@@ -1,18 +1,18 @@
 // lds_chain.hpp - one thread's in-order f32 sum of a run of LDS values,
-// s + p[0] + p[1] + ... , at close to the issue rate of the dependent add.
+// s + p[0] + p[1] + ... , at close to the issue rate of the wave.
 //
-// A wave issues about one instruction per 4.5 cycles, and a dependent
+// A wave issues about one instruction per 4.5 cycles and a dependent
 // v_add_f32 needs no more, so the run costs the adds plus whatever else the
-// wave issues. The LDS reads must also run well ahead of the adds: a read
-// takes longer than many dependent adds, more so while other waves write
-// LDS. Compiled from plain C++, the reads end up next to their use and the
+// wave issues: the LDS reads (one ds_read_b128 per four values) and the
+// waits. Compiled from plain C++, the reads end up next to their use and the
 // chain waits on nearly every one. So the run is written out in assembly:
-// groups of four values, each read by one ds_read_b128 with an immediate
-// offset (no address arithmetic), into eight register sets v96-v127
-// (clobbered) in turn; the read of group g + 7 is issued before the adds of
-// group g, after a single lgkmcnt wait that lets the seven younger reads stay
-// in flight. Every add is a plain v_add_f32 in index order, so the result is
-// bit for bit the sequential one.
+// two sets of sixteen registers, v96-v111 and v112-v127 (clobbered); the
+// four reads of the next set (immediate offsets, no address arithmetic) go
+// out before the sixteen adds of the current one, after a single lgkmcnt
+// wait for the current set. Measured alone on gfx950 this runs at about
+// 6.8 cycles per value (7.5 with a wait per four values). Every add is a
+// plain v_add_f32 in index order, so the result is bit for bit the
+// sequential one.
 #pragma once
 
 #include "device.hpp"
@@ -55,30 +55,11 @@ __device__ __forceinline__ uint32_t lds_addr(const float *p) { return (uint32_t)
 __device__ __forceinline__ float lds_chain64(const float *p, float s) {
     const uint32_t ad = lds_addr(p);
     asm volatile(
-        LC_W(0)
-        LC_R0(0)
-        LC_R1(16)
-        LC_R2(32)
-        LC_R3(48)
-        LC_R4(64)
-        LC_R5(80)
-        LC_R6(96)
-        LC_R7(112) LC_W(7) LC_A0
-        LC_R0(128) LC_W(7) LC_A1
-        LC_R1(144) LC_W(7) LC_A2
-        LC_R2(160) LC_W(7) LC_A3
-        LC_R3(176) LC_W(7) LC_A4
-        LC_R4(192) LC_W(7) LC_A5
-        LC_R5(208) LC_W(7) LC_A6
-        LC_R6(224) LC_W(7) LC_A7
-        LC_R7(240) LC_W(7) LC_A0
-        LC_W(6) LC_A1
-        LC_W(5) LC_A2
-        LC_W(4) LC_A3
-        LC_W(3) LC_A4
-        LC_W(2) LC_A5
-        LC_W(1) LC_A6
-        LC_W(0) LC_A7
+        LC_W(0) LC_R0(0) LC_R1(16) LC_R2(32) LC_R3(48)
+        LC_R4(64) LC_R5(80) LC_R6(96) LC_R7(112) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(128) LC_R1(144) LC_R2(160) LC_R3(176) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(192) LC_R5(208) LC_R6(224) LC_R7(240) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_W(0) LC_A4 LC_A5 LC_A6 LC_A7
         : [o] "+v"(s)
         : [ad] "v"(ad)
         : "memory", LC_CLOBBER);
@@ -89,46 +70,15 @@ __device__ __forceinline__ float lds_chain64(const float *p, float s) {
 __device__ __forceinline__ float lds_chain128(const float *p, float s) {
     const uint32_t ad = lds_addr(p);
     asm volatile(
-        LC_W(0)
-        LC_R0(0)
-        LC_R1(16)
-        LC_R2(32)
-        LC_R3(48)
-        LC_R4(64)
-        LC_R5(80)
-        LC_R6(96)
-        LC_R7(112) LC_W(7) LC_A0
-        LC_R0(128) LC_W(7) LC_A1
-        LC_R1(144) LC_W(7) LC_A2
-        LC_R2(160) LC_W(7) LC_A3
-        LC_R3(176) LC_W(7) LC_A4
-        LC_R4(192) LC_W(7) LC_A5
-        LC_R5(208) LC_W(7) LC_A6
-        LC_R6(224) LC_W(7) LC_A7
-        LC_R7(240) LC_W(7) LC_A0
-        LC_R0(256) LC_W(7) LC_A1
-        LC_R1(272) LC_W(7) LC_A2
-        LC_R2(288) LC_W(7) LC_A3
-        LC_R3(304) LC_W(7) LC_A4
-        LC_R4(320) LC_W(7) LC_A5
-        LC_R5(336) LC_W(7) LC_A6
-        LC_R6(352) LC_W(7) LC_A7
-        LC_R7(368) LC_W(7) LC_A0
-        LC_R0(384) LC_W(7) LC_A1
-        LC_R1(400) LC_W(7) LC_A2
-        LC_R2(416) LC_W(7) LC_A3
-        LC_R3(432) LC_W(7) LC_A4
-        LC_R4(448) LC_W(7) LC_A5
-        LC_R5(464) LC_W(7) LC_A6
-        LC_R6(480) LC_W(7) LC_A7
-        LC_R7(496) LC_W(7) LC_A0
-        LC_W(6) LC_A1
-        LC_W(5) LC_A2
-        LC_W(4) LC_A3
-        LC_W(3) LC_A4
-        LC_W(2) LC_A5
-        LC_W(1) LC_A6
-        LC_W(0) LC_A7
+        LC_W(0) LC_R0(0) LC_R1(16) LC_R2(32) LC_R3(48)
+        LC_R4(64) LC_R5(80) LC_R6(96) LC_R7(112) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(128) LC_R1(144) LC_R2(160) LC_R3(176) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(192) LC_R5(208) LC_R6(224) LC_R7(240) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(256) LC_R1(272) LC_R2(288) LC_R3(304) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(320) LC_R5(336) LC_R6(352) LC_R7(368) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(384) LC_R1(400) LC_R2(416) LC_R3(432) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(448) LC_R5(464) LC_R6(480) LC_R7(496) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_W(0) LC_A4 LC_A5 LC_A6 LC_A7
         : [o] "+v"(s)
         : [ad] "v"(ad)
         : "memory", LC_CLOBBER);
@@ -139,62 +89,81 @@ __device__ __forceinline__ float lds_chain128(const float *p, float s) {
 __device__ __forceinline__ float lds_chain192(const float *p, float s) {
     const uint32_t ad = lds_addr(p);
     asm volatile(
-        LC_W(0)
-        LC_R0(0)
-        LC_R1(16)
-        LC_R2(32)
-        LC_R3(48)
-        LC_R4(64)
-        LC_R5(80)
-        LC_R6(96)
-        LC_R7(112) LC_W(7) LC_A0
-        LC_R0(128) LC_W(7) LC_A1
-        LC_R1(144) LC_W(7) LC_A2
-        LC_R2(160) LC_W(7) LC_A3
-        LC_R3(176) LC_W(7) LC_A4
-        LC_R4(192) LC_W(7) LC_A5
-        LC_R5(208) LC_W(7) LC_A6
-        LC_R6(224) LC_W(7) LC_A7
-        LC_R7(240) LC_W(7) LC_A0
-        LC_R0(256) LC_W(7) LC_A1
-        LC_R1(272) LC_W(7) LC_A2
-        LC_R2(288) LC_W(7) LC_A3
-        LC_R3(304) LC_W(7) LC_A4
-        LC_R4(320) LC_W(7) LC_A5
-        LC_R5(336) LC_W(7) LC_A6
-        LC_R6(352) LC_W(7) LC_A7
-        LC_R7(368) LC_W(7) LC_A0
-        LC_R0(384) LC_W(7) LC_A1
-        LC_R1(400) LC_W(7) LC_A2
-        LC_R2(416) LC_W(7) LC_A3
-        LC_R3(432) LC_W(7) LC_A4
-        LC_R4(448) LC_W(7) LC_A5
-        LC_R5(464) LC_W(7) LC_A6
-        LC_R6(480) LC_W(7) LC_A7
-        LC_R7(496) LC_W(7) LC_A0
-        LC_R0(512) LC_W(7) LC_A1
-        LC_R1(528) LC_W(7) LC_A2
-        LC_R2(544) LC_W(7) LC_A3
-        LC_R3(560) LC_W(7) LC_A4
-        LC_R4(576) LC_W(7) LC_A5
-        LC_R5(592) LC_W(7) LC_A6
-        LC_R6(608) LC_W(7) LC_A7
-        LC_R7(624) LC_W(7) LC_A0
-        LC_R0(640) LC_W(7) LC_A1
-        LC_R1(656) LC_W(7) LC_A2
-        LC_R2(672) LC_W(7) LC_A3
-        LC_R3(688) LC_W(7) LC_A4
-        LC_R4(704) LC_W(7) LC_A5
-        LC_R5(720) LC_W(7) LC_A6
-        LC_R6(736) LC_W(7) LC_A7
-        LC_R7(752) LC_W(7) LC_A0
-        LC_W(6) LC_A1
-        LC_W(5) LC_A2
-        LC_W(4) LC_A3
-        LC_W(3) LC_A4
-        LC_W(2) LC_A5
-        LC_W(1) LC_A6
-        LC_W(0) LC_A7
+        LC_W(0) LC_R0(0) LC_R1(16) LC_R2(32) LC_R3(48)
+        LC_R4(64) LC_R5(80) LC_R6(96) LC_R7(112) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(128) LC_R1(144) LC_R2(160) LC_R3(176) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(192) LC_R5(208) LC_R6(224) LC_R7(240) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(256) LC_R1(272) LC_R2(288) LC_R3(304) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(320) LC_R5(336) LC_R6(352) LC_R7(368) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(384) LC_R1(400) LC_R2(416) LC_R3(432) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(448) LC_R5(464) LC_R6(480) LC_R7(496) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(512) LC_R1(528) LC_R2(544) LC_R3(560) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(576) LC_R5(592) LC_R6(608) LC_R7(624) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(640) LC_R1(656) LC_R2(672) LC_R3(688) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(704) LC_R5(720) LC_R6(736) LC_R7(752) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_W(0) LC_A4 LC_A5 LC_A6 LC_A7
+        : [o] "+v"(s)
+        : [ad] "v"(ad)
+        : "memory", LC_CLOBBER);
+    return s;
+}
+
+// s + p[0..255] in order (p in LDS, 16-byte aligned).
+__device__ __forceinline__ float lds_chain256(const float *p, float s) {
+    const uint32_t ad = lds_addr(p);
+    asm volatile(
+        LC_W(0) LC_R0(0) LC_R1(16) LC_R2(32) LC_R3(48)
+        LC_R4(64) LC_R5(80) LC_R6(96) LC_R7(112) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(128) LC_R1(144) LC_R2(160) LC_R3(176) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(192) LC_R5(208) LC_R6(224) LC_R7(240) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(256) LC_R1(272) LC_R2(288) LC_R3(304) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(320) LC_R5(336) LC_R6(352) LC_R7(368) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(384) LC_R1(400) LC_R2(416) LC_R3(432) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(448) LC_R5(464) LC_R6(480) LC_R7(496) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(512) LC_R1(528) LC_R2(544) LC_R3(560) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(576) LC_R5(592) LC_R6(608) LC_R7(624) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(640) LC_R1(656) LC_R2(672) LC_R3(688) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(704) LC_R5(720) LC_R6(736) LC_R7(752) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(768) LC_R1(784) LC_R2(800) LC_R3(816) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(832) LC_R5(848) LC_R6(864) LC_R7(880) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(896) LC_R1(912) LC_R2(928) LC_R3(944) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(960) LC_R5(976) LC_R6(992) LC_R7(1008) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_W(0) LC_A4 LC_A5 LC_A6 LC_A7
+        : [o] "+v"(s)
+        : [ad] "v"(ad)
+        : "memory", LC_CLOBBER);
+    return s;
+}
+
+// s + p[0..383] in order (p in LDS, 16-byte aligned).
+__device__ __forceinline__ float lds_chain384(const float *p, float s) {
+    const uint32_t ad = lds_addr(p);
+    asm volatile(
+        LC_W(0) LC_R0(0) LC_R1(16) LC_R2(32) LC_R3(48)
+        LC_R4(64) LC_R5(80) LC_R6(96) LC_R7(112) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(128) LC_R1(144) LC_R2(160) LC_R3(176) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(192) LC_R5(208) LC_R6(224) LC_R7(240) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(256) LC_R1(272) LC_R2(288) LC_R3(304) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(320) LC_R5(336) LC_R6(352) LC_R7(368) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(384) LC_R1(400) LC_R2(416) LC_R3(432) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(448) LC_R5(464) LC_R6(480) LC_R7(496) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(512) LC_R1(528) LC_R2(544) LC_R3(560) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(576) LC_R5(592) LC_R6(608) LC_R7(624) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(640) LC_R1(656) LC_R2(672) LC_R3(688) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(704) LC_R5(720) LC_R6(736) LC_R7(752) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(768) LC_R1(784) LC_R2(800) LC_R3(816) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(832) LC_R5(848) LC_R6(864) LC_R7(880) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(896) LC_R1(912) LC_R2(928) LC_R3(944) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(960) LC_R5(976) LC_R6(992) LC_R7(1008) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(1024) LC_R1(1040) LC_R2(1056) LC_R3(1072) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(1088) LC_R5(1104) LC_R6(1120) LC_R7(1136) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(1152) LC_R1(1168) LC_R2(1184) LC_R3(1200) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(1216) LC_R5(1232) LC_R6(1248) LC_R7(1264) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(1280) LC_R1(1296) LC_R2(1312) LC_R3(1328) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(1344) LC_R5(1360) LC_R6(1376) LC_R7(1392) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_R0(1408) LC_R1(1424) LC_R2(1440) LC_R3(1456) LC_W(4) LC_A4 LC_A5 LC_A6 LC_A7
+        LC_R4(1472) LC_R5(1488) LC_R6(1504) LC_R7(1520) LC_W(4) LC_A0 LC_A1 LC_A2 LC_A3
+        LC_W(0) LC_A4 LC_A5 LC_A6 LC_A7
         : [o] "+v"(s)
         : [ad] "v"(ad)
         : "memory", LC_CLOBBER);

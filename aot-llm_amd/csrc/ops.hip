@@ -658,8 +658,10 @@ __global__ __launch_bounds__(HD == 256 ? 64 * (QKD_MAX_GQA_256 + 1) : 576) void 
 //   output (ops.rs:209-215): chunks of CP positions: all threads form the
 //   products p_t * v_t,d into LDS, dim-major (row of dim d: CP products and
 //   4 pad floats), with the float4 V loads issued PD chunks ahead; then
-//   thread d adds its row in position order (float4 LDS reads one group of
-//   16 ahead of the adds) while the others form the next chunk.
+//   thread d adds its row in position order (lds_chain) while the others
+//   form the next chunk. Sixteen dims per block put 8 blocks on every head
+//   (256 for 32 heads); chunks of 384 positions halve the barriers per
+//   position against 192.
 #ifndef ATT_TS
 #define ATT_TS(i)
 #endif
@@ -667,8 +669,8 @@ __global__ __launch_bounds__(HD == 256 ? 64 * (QKD_MAX_GQA_256 + 1) : 576) void 
 #define SV_TS(c, i)
 #endif
 constexpr int ATT_MAX_SPAN = 16384;
-constexpr int SV_DB = 32;         // dims per block
-constexpr int SV_CP = 192;        // positions per chunk
+constexpr int SV_DB = 16;         // dims per block
+constexpr int SV_CP = 384;        // positions per chunk
 constexpr int SV_RS = SV_CP + 4;  // floats per dim row of the product buffer
 constexpr int SV_BUF = SV_DB * SV_RS;  // floats per product buffer
 constexpr int SV_SEQ_MIN = 512;  // shorter spans are summed by one thread
@@ -702,7 +704,7 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     // are dealt to the 4 SIMDs in turn) form them, so the dependent adds
     // issue back to back
     constexpr int NPROD = (SEQ_T / 64 - SEQ_T / 256) * 64;
-    static_assert(CP == 192, "the output adds of a full chunk run in lds_chain192");
+    static_assert(CP == 384, "the output adds of a full chunk run in lds_chain384");
     static_assert(CP * R4 == 2 * NPROD, "two float4 per producer thread per chunk");
     // V loads run PD chunks ahead of the products (a register ring)
     constexpr int PD = 8;
@@ -788,7 +790,10 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
                 if (tid < DB) {
                     // the chunk's rows rounded up to 64 (the padding adds -0.0)
                     const float *tp = buf + tid * SV_RS;
-                    if (rows > 128) o = lds_chain192(tp, o);
+                    if (rows > 320) o = lds_chain384(tp, o);
+                    else if (rows > 256) o = lds_chain128(tp + 192, lds_chain192(tp, o));
+                    else if (rows > 192) o = lds_chain256(tp, o);
+                    else if (rows > 128) o = lds_chain192(tp, o);
                     else if (rows > 64) o = lds_chain128(tp, o);
                     else o = lds_chain64(tp, o);
                 }
