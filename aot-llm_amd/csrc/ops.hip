@@ -673,7 +673,7 @@ constexpr int SV_DB = 16;         // dims per block
 constexpr int SV_CP = 384;        // positions per chunk
 constexpr int SV_RS = SV_CP + 4;  // floats per dim row of the product buffer
 constexpr int SV_BUF = SV_DB * SV_RS;  // floats per product buffer
-constexpr int SV_SEQ_MIN = 512;  // shorter spans are summed by one thread
+constexpr int SV_SEQ_MIN = 1024;  // shorter spans are summed by one thread
 template <int HD>
 __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     constexpr int DB = SV_DB;
