@@ -125,8 +125,8 @@ __device__ __forceinline__ float pow2f(int e) { return __int_as_float((127 + e) 
 
 // Walk of the steps on one wave, 64 at a time. Every lane runs the same
 // chain of plain f32 adds over the batch (the values read as LDS
-// broadcasts, four per read) and keeps the running sum before step j in
-// lane j; afterwards every lane checks its own run in parallel (s in
+// broadcasts, four per read); lane j recovers the running sum before step
+// j; afterwards every lane checks its own run in parallel (s in
 // [2^e, 2^(e+1)) and s + G * 2^(e-23) < 2^(e+1): then the add was the exact
 // jump A += G). At the first failed check the walk restarts from that step
 // and adds the run's elements one by one.
@@ -151,23 +151,37 @@ __device__ __forceinline__ float seq_walk(const float *pp, int C, int total, con
             if (skip > 2) av[0].z = 0.0f;
         }
         const bool mine = lane >= skip && lane < cnt;
-        const float myadd = mine ? S.sa[eb + lane] : 0.0f;
+        // this lane's group of four steps (the skipped ones added as 0, as in the chain)
+        float4 gv = reinterpret_cast<const float4 *>(S.sa + eb)[lane >> 2];
+        if (lane < 4) {
+            if (skip > 0) gv.x = 0.0f;
+            if (skip > 1) gv.y = 0.0f;
+            if (skip > 2) gv.z = 0.0f;
+        }
         const float mylo = mine ? S.slo[eb + lane] : 0.0f;
         const int myz = lane < cnt ? S.sz[eb + lane] : 0;
+        // the chain keeps the sum before every fourth step in that group's
+        // four lanes; each lane then adds its group's steps before its own,
+        // in order (the same adds as the chain, so the same roundings)
         float t = s, hist = s;
+        const int grp = lane >> 2, r = lane & 3;
         SEQ_TS(7);
 #pragma unroll
-        for (int q = 0; q < 16; q++) {
-            if (4 * q >= cnt) break;
-            hist = lane == 4 * q ? t : hist;
-            t += av[q].x;
-            hist = lane == 4 * q + 1 ? t : hist;
-            t += av[q].y;
-            hist = lane == 4 * q + 2 ? t : hist;
-            t += av[q].z;
-            hist = lane == 4 * q + 3 ? t : hist;
-            t += av[q].w;
+        for (int q16 = 0; q16 < 4; q16++) {
+            if (16 * q16 >= cnt) break;  // (steps past the total add 0)
+#pragma unroll
+            for (int q = 4 * q16; q < 4 * q16 + 4; q++) {
+                hist = grp == q ? t : hist;
+                t += av[q].x;
+                t += av[q].y;
+                t += av[q].z;
+                t += av[q].w;
+            }
         }
+        if (r > 0) hist += gv.x;
+        if (r > 1) hist += gv.y;
+        if (r > 2) hist += gv.z;
+        const float myadd = r == 0 ? gv.x : (r == 1 ? gv.y : (r == 2 ? gv.z : gv.w));
         SEQ_TS(8);
         const bool ok = mylo == 0.0f || (hist >= mylo && hist + myadd < 2.0f * mylo);
         const unsigned long long bad = __ballot(!ok && mine);
