@@ -142,10 +142,17 @@ __device__ __forceinline__ bool exc_lookup(const uint32_t (*tab)[2], int n, uint
 }
 
 // expf / tanhf bit-identical to the host libm the reference links against.
-__device__ __forceinline__ float aotk_expf(float x) {
+// aotk_expf_tab reads the 2^(i/32) table from a copy (exp_table_to_lds: in
+// LDS a lookup costs an LDS read instead of a constant-memory load).
+__device__ __forceinline__ float aotk_expf_tab(float x, const uint64_t *tab) {
     uint32_t o;
     if (AOTK_EXPF_EXC_N && exc_lookup(expf_exc, AOTK_EXPF_EXC_N, __float_as_uint(x), o)) return __uint_as_float(o);
-    return lm_expf(x);
+    return lm_expf_tab(x, tab);
+}
+__device__ __forceinline__ float aotk_expf(float x) { return aotk_expf_tab(x, lm_exp2f_tab_dev); }
+// The first 32 threads copy the table (the caller synchronises before use).
+__device__ __forceinline__ void exp_table_to_lds(uint64_t *dst) {
+    if (threadIdx.x < 32) dst[threadIdx.x] = lm_exp2f_tab_dev[threadIdx.x];
 }
 __device__ __forceinline__ float aotk_tanhf(float x) {
     uint32_t o;

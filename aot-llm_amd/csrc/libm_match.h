@@ -85,12 +85,8 @@ static const uint64_t lm_exp2f_tab_host[32] = {
 0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
 0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
 
-LM_FN float lm_expf(float x) {
-#ifdef __HIP_DEVICE_COMPILE__
-    const uint64_t *tab = lm_exp2f_tab_dev;
-#else
-    const uint64_t *tab = lm_exp2f_tab_host;
-#endif
+/* tab: the 32-entry table (a copy of it, e.g. in LDS on the device) */
+LM_FN float lm_expf_tab(float x, const uint64_t *tab) {
     const double invln2n = 0x1.71547652b82fep+0 * 32;
     const double shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32, c2 = 0x1.62e42ff0c52d6p-1 / 32;
@@ -116,6 +112,14 @@ LM_FN float lm_expf(float x) {
     y = lm_fma(zz, r2, y);
     y = y * s;
     return (float)y;
+}
+
+LM_FN float lm_expf(float x) {
+#ifdef __HIP_DEVICE_COMPILE__
+    return lm_expf_tab(x, lm_exp2f_tab_dev);
+#else
+    return lm_expf_tab(x, lm_exp2f_tab_host);
+#endif
 }
 
 /* ---- tanhf: fdlibm's s_tanhf.c / s_expm1f.c (Sun Microsystems, the

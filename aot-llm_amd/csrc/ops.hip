@@ -683,6 +683,7 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     __shared__ __align__(16) uint8_t ubuf[sizeof(SeqScratch) > (2 * SV_BUF + 64) * 4 ? sizeof(SeqScratch) : (2 * SV_BUF + 64) * 4];
     __shared__ float red[SEQ_T / 64];
     __shared__ float bc;
+    __shared__ uint64_t stab[32];  // expf's 2^(i/32) table
     SeqScratch &S = *reinterpret_cast<SeqScratch *>(ubuf);
     float *prod = reinterpret_cast<float *>(ubuf);
     const int tid = threadIdx.x, lane = tid & 63;
@@ -726,18 +727,29 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < PE; j++) issue(ring[j], j);
     ATT_TS(0);
+    // the scores stay in registers (all loads in flight together) through
+    // the max; the exps, independent of each other, interleave
+    constexpr int SPT = ATT_MAX_SPAN / SEQ_T;  // scores per thread
+    exp_table_to_lds(stab);
+    float sv[SPT];
     float mx = -INFINITY;
-    for (int t = tid; t < cnt; t += SEQ_T) {
-        const float v = ps[t];
-        e[at(t)] = v;
-        mx = fmaxf(mx, v);
+#pragma unroll
+    for (int k = 0; k < SPT; k++) {
+        const int t = tid + k * SEQ_T;
+        sv[k] = t < cnt ? ps[t] : -INFINITY;
     }
+#pragma unroll
+    for (int k = 0; k < SPT; k++) mx = fmaxf(mx, sv[k]);
     mx = wave_max(mx);
     if (lane == 0) red[tid >> 6] = mx;
     __syncthreads();
     mx = wave_max(lane < SEQ_T / 64 ? red[lane] : -INFINITY);
     ATT_TS(1);
-    for (int t = tid; t < cnt; t += SEQ_T) e[at(t)] = aotk_expf(e[at(t)] - mx);
+#pragma unroll
+    for (int k = 0; k < SPT; k++) {
+        const int t = tid + k * SEQ_T;
+        if (t < cnt) e[at(t)] = aotk_expf_tab(sv[k] - mx, stab);
+    }
     // the one-thread sum runs over whole runs of 64: the positions past the
     // span up to the next multiple of 64 hold -0.0, which leaves it unchanged
     if (!exact && tid < 64 && cnt + tid < ((cnt + 63) & ~63)) e[cnt + tid] = -0.0f;
