@@ -582,6 +582,76 @@ __global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq2(MvArgs a, int RLa, i
     else mv_kq_body<KB, PF, NB>(b, RLb, Gb, blockIdx.x - nblk_a, sh.y, sh.t);
 }
 
+// Rows of 33..64 super-blocks on two waves each: wave 2r + w of the block
+// takes super-blocks 32w .. 32w + 31 of row r, each split over a lane pair
+// as for short rows (the same SPL = 2 term); the terms meet in LDS and one
+// lane folds the row in super-block order. Half the per-lane work of one
+// lane per whole super-block, on twice the waves (Q6_K 4096x14336: 11.9
+// against 13.5 us).
+template <int KIND, int NB>
+__global__ __launch_bounds__(256) void k_mv_kqw(MvArgs a) {
+    static_assert(NB > 32 && NB <= 64, "rows of 33..64 super-blocks");
+    __shared__ __align__(16) uint8_t sY[64 * KQ_REC];
+    __shared__ __align__(16) float sT[2][64];
+    using Geo = KqGeom<KIND>;
+    constexpr int CH = kq_chl<KIND, 2>();
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tok = blockIdx.y;
+    const int h = lane & 1;
+    const int s = 32 * (wave & 1) + (lane >> 1);
+    const bool lane_on = s < NB;
+    const int sa = lane_on ? s : 0;
+    const int rslot = wave >> 1;
+    const int row = blockIdx.x * 2 + rslot;
+    const bool row_on = row < a.total_rows;
+    constexpr size_t cs = (size_t)NB * 16;
+    constexpr size_t rowb = (size_t)NB * Geo::RB;
+    // the activation first (as mv_kq_body), then the weights
+    constexpr int nq = NB * 16;
+    const uint4 *xq = (const uint4 *)(a.xq + (size_t)tok * a.cols);
+    const uint4 *xb = (const uint4 *)(a.xbs + (size_t)tok * NB * 16);
+    uint4 xv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) xv[k] = xq[min(tid + 256 * k, nq - 1)];
+    const uint4 bv = xb[min(tid, 2 * NB - 1)];
+    const float dv = a.xd[(size_t)tok * NB + min(tid, NB - 1)];
+    // rows past the end load row 0 (valid memory); they are never stored
+    int local;
+    const int sg = seg_of(a, row_on ? row : 0, local);
+    const uint8_t *wp = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * rowb + (size_t)sa * 16;
+    uint4 c[CH];
+#pragma unroll
+    for (int k = 0; k < CH; k++) c[k] = *(const uint4 *)(wp + kq_chunk<KIND, 2>(k, h) * cs);
+    float d6 = 0.0f;
+    if (KIND == AOTK_Q6_K) d6 = f16_to_f32(((const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]))[(size_t)local * NB + sa]);
+    // unconditional stores: past the end they repeat the last element
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = min(tid + 256 * k, nq - 1);
+        *(uint4 *)(sY + (i >> 4) * KQ_REC + (i & 15) * 16) = xv[k];
+    }
+    const int ib = min(tid, 2 * NB - 1);
+    *(uint4 *)(sY + (ib >> 1) * KQ_REC + 256 + (ib & 1) * 16) = bv;
+    *(float *)(sY + min(tid, NB - 1) * KQ_REC + 288) = dv;
+    __syncthreads();
+    const float term = kq_term<KIND, 2>(c, d6, sY + sa * KQ_REC, h);
+    if (lane_on && h == 0) sT[rslot][s] = term;
+    __syncthreads();
+    if ((wave & 1) == 0 && lane == 0 && row_on) {
+        const float4 *tp = (const float4 *)sT[rslot];
+        float acc = 0.0f;
+#pragma unroll
+        for (int q = 0; q < (NB + 3) / 4; q++) {
+            const float4 v = tp[q];
+            acc = acc + v.x;
+            if (4 * q + 1 < NB) acc = acc + v.y;
+            if (4 * q + 2 < NB) acc = acc + v.z;
+            if (4 * q + 3 < NB) acc = acc + v.w;
+        }
+        store_row(a, row, tok, acc);
+    }
+}
+
 // The row lengths of the configs (cols / 256) get their own instantiations.
 #define AOTK_NB_SWITCH(nb, F) \
     switch (nb) {             \
@@ -1915,6 +1985,15 @@ static void kq_shape(const MvArgs &a, int &RL, int &G, int &blocks) {
 
 template <int KIND>
 static void launch_kq(const MvArgs &a, dim3 grid, hipStream_t s) {
+    // Q6_K rows of 40..56 super-blocks: two waves per row (the lighter
+    // Q4_K / Q5_K terms measured faster on one lane per super-block)
+    if (KIND == AOTK_Q6_K && !a.xq_src && (a.nb == 40 || a.nb == 48 || a.nb == 56)) {
+        grid.x = (unsigned)((a.total_rows + 1) / 2);
+        if (a.nb == 40) k_mv_kqw<KIND, 40><<<grid, 256, 0, s>>>(a);
+        else if (a.nb == 48) k_mv_kqw<KIND, 48><<<grid, 256, 0, s>>>(a);
+        else k_mv_kqw<KIND, 56><<<grid, 256, 0, s>>>(a);
+        return;
+    }
     if (a.nb <= 64) {
         int RL, G, blocks;
         kq_shape(a, RL, G, blocks);
