@@ -196,8 +196,61 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant(const float *__restrict
     RMS_TS(3);
 }
 
+// Rows of whole 256-value blocks: thread t holds float4 t (+ 1024 k) of the
+// row, so wave w holds the values of quantization blocks w (+ 16 k) in
+// quant256's lane order: the normalised row goes from registers straight
+// to the quantizer, with no LDS copy and no barrier after the sum.
+template <int KF>
+__global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant4(const float *__restrict__ x, const float *__restrict__ w, int n,
+                                                         float eps, RmsOut out) {
+    __shared__ float sq[SEQ_PAD_N];
+    __shared__ SeqScratch S;
+    const size_t m = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int n4 = n / 4;
+    const int C = seq_chunk(n);
+    const float4 *xr = (const float4 *)(x + m * n);
+    float4 xv[KF], wv[KF];
+#pragma unroll
+    for (int k = 0; k < KF; k++) {
+        const int i = tid + k * SEQ_T;
+        xv[k] = i < n4 ? xr[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int k = 0; k < KF; k++) {
+        const int i = tid + k * SEQ_T;
+        wv[k] = i < n4 ? ((const float4 *)w)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int k = 0; k < KF; k++) {
+        const int i = tid + k * SEQ_T;
+        if (i < n4) {
+            sq[seq_idx(4 * i, C)] = xv[k].x * xv[k].x;
+            sq[seq_idx(4 * i + 1, C)] = xv[k].y * xv[k].y;
+            sq[seq_idx(4 * i + 2, C)] = xv[k].z * xv[k].z;
+            sq[seq_idx(4 * i + 3, C)] = xv[k].w * xv[k].w;
+        }
+    }
+    __syncthreads();
+    const float ss = exact_seq_sum(sq, n, S);
+    const float r = 1.0f / sqrtf(ss / (float)n + eps);
+    const ActQ8K qk = q8k_row(out.q8k, m, n);
+    const ActQ8_0 q0 = q80_row(out.q80, m, n);
+#pragma unroll
+    for (int k = 0; k < KF; k++) {
+        const int i = tid + k * SEQ_T;
+        if (i < n4) {  // wave-uniform: n4 is a multiple of 64
+            const float v[4] = {xv[k].x * r * wv[k].x, xv[k].y * r * wv[k].y, xv[k].z * r * wv[k].z, xv[k].w * r * wv[k].w};
+            if (out.f32) *(float4 *)(out.f32 + m * n + 4 * i) = make_float4(v[0], v[1], v[2], v[3]);
+            quant256(v, lane, (size_t)(i >> 6), qk, q0);
+        }
+    }
+}
+
 void launch_rmsnorm_quant(const float *x, const float *w, size_t n, size_t m, float eps, RmsOut out, hipStream_t s) {
-    k_rmsnorm_quant<<<(unsigned)m, SEQ_T, 0, s>>>(x, w, (int)n, eps, out);
+    if (n % 256 == 0 && n <= 4096) k_rmsnorm_quant4<1><<<(unsigned)m, SEQ_T, 0, s>>>(x, w, (int)n, eps, out);
+    else if (n % 256 == 0) k_rmsnorm_quant4<2><<<(unsigned)m, SEQ_T, 0, s>>>(x, w, (int)n, eps, out);
+    else k_rmsnorm_quant<<<(unsigned)m, SEQ_T, 0, s>>>(x, w, (int)n, eps, out);
 }
 
 // Quantize m rows of n floats (n % 256 == 0), one wave per 256 values.
