@@ -1210,9 +1210,78 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_add_quant(float *x, const flo
     }
 }
 
+// The same for rows of whole 256-blocks, float4 per thread as in
+// k_rmsnorm_quant4 (the joined row quantized from registers).
+template <int KF>
+__global__ __launch_bounds__(SEQ_T) void k_rmsnorm_add_quant4(float *x, const float *y, const float *w_post,
+                                                              const float *w_next, int n, float eps, RmsOut out) {
+    __shared__ float sq[SEQ_PAD_N];
+    __shared__ SeqScratch S;
+    const size_t m = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int n4 = n / 4;
+    const int C = seq_chunk(n);
+    float4 *xr = (float4 *)(x + m * n);
+    const float4 *yr = (const float4 *)(y + m * n);
+    float4 yv[KF], xv[KF], wv[KF], wn[KF];
+    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int k = 0; k < KF; k++) yv[k] = tid + k * SEQ_T < n4 ? yr[tid + k * SEQ_T] : z;
+#pragma unroll
+    for (int k = 0; k < KF; k++) xv[k] = tid + k * SEQ_T < n4 ? xr[tid + k * SEQ_T] : z;
+#pragma unroll
+    for (int k = 0; k < KF; k++) wv[k] = tid + k * SEQ_T < n4 ? ((const float4 *)w_post)[tid + k * SEQ_T] : z;
+#pragma unroll
+    for (int k = 0; k < KF; k++) wn[k] = tid + k * SEQ_T < n4 ? ((const float4 *)w_next)[tid + k * SEQ_T] : z;
+    auto squares = [&](const float4 &v, int i) {
+        sq[seq_idx(4 * i, C)] = v.x * v.x;
+        sq[seq_idx(4 * i + 1, C)] = v.y * v.y;
+        sq[seq_idx(4 * i + 2, C)] = v.z * v.z;
+        sq[seq_idx(4 * i + 3, C)] = v.w * v.w;
+    };
+#pragma unroll
+    for (int k = 0; k < KF; k++)
+        if (tid + k * SEQ_T < n4) squares(yv[k], tid + k * SEQ_T);
+    __syncthreads();
+    const float ss = exact_seq_sum(sq, n, S);
+    const float r = 1.0f / sqrtf(ss / (float)n + eps);
+    // x += y * r * w (as k_rmsnorm_add), then the squares of the new x
+    // (exact_seq_sum's closing barrier orders these writes after its reads)
+#pragma unroll
+    for (int k = 0; k < KF; k++) {
+        const int i = tid + k * SEQ_T;
+        if (i < n4) {
+            float4 v;
+            v.x = xv[k].x + yv[k].x * r * wv[k].x;
+            v.y = xv[k].y + yv[k].y * r * wv[k].y;
+            v.z = xv[k].z + yv[k].z * r * wv[k].z;
+            v.w = xv[k].w + yv[k].w * r * wv[k].w;
+            xv[k] = v;
+            xr[i] = v;
+            squares(v, i);
+        }
+    }
+    __syncthreads();
+    const float ss2 = exact_seq_sum(sq, n, S);
+    const float r2 = 1.0f / sqrtf(ss2 / (float)n + eps);
+    const ActQ8K qk = q8k_row(out.q8k, m, n);
+    const ActQ8_0 q0 = q80_row(out.q80, m, n);
+#pragma unroll
+    for (int k = 0; k < KF; k++) {
+        const int i = tid + k * SEQ_T;
+        if (i < n4) {  // wave-uniform: n4 is a multiple of 64
+            const float v[4] = {xv[k].x * r2 * wn[k].x, xv[k].y * r2 * wn[k].y, xv[k].z * r2 * wn[k].z, xv[k].w * r2 * wn[k].w};
+            if (out.f32) *(float4 *)(out.f32 + m * n + 4 * i) = make_float4(v[0], v[1], v[2], v[3]);
+            quant256(v, lane, (size_t)(i >> 6), qk, q0);
+        }
+    }
+}
+
 void launch_rmsnorm_add_quant(float *x, const float *y, const float *w_post, const float *w_next, size_t n, size_t m,
                               float eps, RmsOut out, hipStream_t s) {
-    k_rmsnorm_add_quant<<<(unsigned)m, SEQ_T, 0, s>>>(x, y, w_post, w_next, (int)n, eps, out);
+    if (n % 256 == 0 && n <= 4096) k_rmsnorm_add_quant4<1><<<(unsigned)m, SEQ_T, 0, s>>>(x, y, w_post, w_next, (int)n, eps, out);
+    else if (n % 256 == 0) k_rmsnorm_add_quant4<2><<<(unsigned)m, SEQ_T, 0, s>>>(x, y, w_post, w_next, (int)n, eps, out);
+    else k_rmsnorm_add_quant<<<(unsigned)m, SEQ_T, 0, s>>>(x, y, w_post, w_next, (int)n, eps, out);
 }
 
 void launch_rmsnorm_add(float *x, const float *y, const float *w, size_t n, size_t m, float eps, hipStream_t s) {
