@@ -15,7 +15,7 @@ def cols_for(kind):
             Q4_0: [32, 96, 2048, 4096, 5632, 14336, 16384, 18432], Q5_0: [32, 96, 2048, 4096, 14336, 16384, 18432],
             Q8_0: [32, 96, 2048, 4096, 12288, 14336, 16384, 18432],
             Q4_K: [256, 512, 2048, 3072, 5632, 14336, 17408], Q5_K: [256, 512, 2560, 4096, 10240, 14336],
-            Q6_K: [256, 512, 2048, 5632, 14336, 17408]}[kind]
+            Q6_K: [256, 512, 2048, 5632, 10240, 12288, 14336, 17408]}[kind]
 
 
 def weights(kind, rows, cols, seed, oracle):
