@@ -872,14 +872,15 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
 
 // Batched rows (prompt chunks), spans up to ATT_MAX_SPAN: the same softmax
 // and output, with the serial chains spread over lanes instead of blocks.
-//   k_attn_softmax_rows: one wave per (row, head): max, glibc-matched exp
-//   into LDS, the sequential sum by lane 0, then p = e * (1 / sum) written
-//   back over the scores.
+//   k_attn_softmax_rows: one wave per (row, head) for spans up to
+//   ATT_ROWS_MAX: max, glibc-matched exp into LDS, the sequential sum by
+//   lane 0, then p = e * (1 / sum) written back over the scores; longer
+//   spans: k_attn_softmax_rows_x, a block per (row, head).
 //   k_attn_out_rows: one wave per (head, 64-dim slice, ATT_RB rows); lane d
 //   keeps the ATT_RB sums of dim d and adds p_t * v_t,d in position order;
 //   V rows are read straight from the cache (256 B per wave per position),
 //   the probabilities with wave-uniform loads.
-constexpr int ATT_ROWS_MAX = 2048;  // spans of the 4-wave softmax blocks (one wave per block up to ATT_MAX_SPAN)
+constexpr int ATT_ROWS_MAX = 2048;  // spans of the one-wave softmax (four waves per block)
 constexpr int ATT_RB = 4;
 
 template <int NW, int CAP>
@@ -1003,11 +1004,59 @@ __global__ __launch_bounds__(256) void k_attn_out_rows(AttnArgs a, int m) {
         if (rg * ATT_RB + r < m) a.out[(size_t)row[r] * a.n_head * HD + (size_t)h * HD + d] = o[r];
 }
 
+// The same for rows of more than ATT_ROWS_MAX positions: a block of SEQ_T
+// threads per (row, head), the scores held in registers through the max,
+// the exps with the 2^(i/32) table in LDS, the exact parallel replay of the
+// sequential sum (one wave's single-thread sum of 4096 terms took ~100 us).
+template <int CAP>
+__global__ __launch_bounds__(SEQ_T) void k_attn_softmax_rows_x(AttnArgs a, int m) {
+    __shared__ __align__(16) float e[CAP + SEQ_T + 32];
+    __shared__ SeqScratch S;
+    __shared__ float red[SEQ_T / 64];
+    __shared__ uint64_t stab[32];
+    constexpr int SPT = CAP / SEQ_T;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int i = blockIdx.x / a.n_head, h = blockIdx.x % a.n_head;
+    size_t t0, n;
+    row_range(a, i, t0, n);
+    const int cnt = (int)(n - t0);
+    float *ps = a.prob + ((size_t)i * a.n_head + h) * a.span;
+    exp_table_to_lds(stab);
+    float sv[SPT];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < SPT; k++) {
+        const int t = tid + k * SEQ_T;
+        sv[k] = t < cnt ? ps[t] : -INFINITY;
+        mx = fmaxf(mx, sv[k]);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = wave_max(lane < SEQ_T / 64 ? red[lane] : -INFINITY);
+    const int C = seq_chunk(cnt);
+#pragma unroll
+    for (int k = 0; k < SPT; k++) {
+        const int t = tid + k * SEQ_T;
+        if (t < cnt) {
+            sv[k] = aotk_expf_tab(sv[k] - mx, stab);
+            e[seq_idx(t, C)] = sv[k];
+        }
+    }
+    __syncthreads();
+    const float inv = 1.0f / exact_seq_sum(e, cnt, S);
+#pragma unroll
+    for (int k = 0; k < SPT; k++) {
+        const int t = tid + k * SEQ_T;
+        if (t < cnt) ps[t] = sv[k] * inv;
+    }
+}
+
 static void launch_rows(const AttnArgs &a, size_t head_dim, size_t m, size_t longest, hipStream_t s) {
     const unsigned pairs = (unsigned)(m * a.n_head);
     if (longest <= (size_t)ATT_ROWS_MAX) k_attn_softmax_rows<4, ATT_ROWS_MAX><<<(pairs + 3) / 4, 256, 0, s>>>(a, (int)m);
-    else if (longest <= 8192) k_attn_softmax_rows<1, 8192><<<pairs, 64, 0, s>>>(a, (int)m);
-    else k_attn_softmax_rows<1, ATT_MAX_SPAN><<<pairs, 64, 0, s>>>(a, (int)m);
+    else if (longest <= 8192) k_attn_softmax_rows_x<8192><<<pairs, SEQ_T, 0, s>>>(a, (int)m);
+    else k_attn_softmax_rows_x<ATT_MAX_SPAN><<<pairs, SEQ_T, 0, s>>>(a, (int)m);
     const size_t tasks = (m + ATT_RB - 1) / ATT_RB * a.n_head * (head_dim / 64);
     const unsigned g = (unsigned)((tasks + 3) / 4);
     switch (head_dim) {
