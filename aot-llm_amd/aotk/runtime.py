@@ -106,6 +106,17 @@ def time_matvec(weights, x, iters):
     return ms.value
 
 
+def time_matmul(weights, xs, iters):
+    """Mean device ms per batched product of the m rows of `xs` (m x cols
+    f32, quantized once on the device), rotating over `weights`."""
+    xs = np.ascontiguousarray(xs, np.float32)
+    dx = DeviceBuffer.from_numpy(xs)
+    arr = (C.c_void_p * len(weights))(*[w.h for w in weights])
+    ms = C.c_float()
+    abi.check(_lib().aotk_time_matmul(arr, len(weights), dx.ptr, xs.shape[0], iters, C.byref(ms)))
+    return ms.value
+
+
 def dequant_rows(w, row0=0, n_rows=None):
     n_rows = w.rows - row0 if n_rows is None else n_rows
     out = DeviceBuffer(n_rows * w.cols * 4)

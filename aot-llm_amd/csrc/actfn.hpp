@@ -86,6 +86,10 @@ __device__ __forceinline__ void quant256(const float v[4], int lane, size_t blk,
     if (q8k.qs) {
         const Q8KLane r = q8k_lane(v, lane);
         ((uint32_t *)(q8k.qs + blk * 256))[lane] = r.packed;
+        if (q8k.qt) {  // the tiled copy: elements 4*lane .. +3 are one aligned 4-byte run there
+            const size_t v = (size_t)q8k.tok + blk / q8k.nbt;
+            *(uint32_t *)(q8k.qt + q8k_tiled_off(v, (int)(blk % q8k.nbt), q8k.nbt, 4 * lane)) = r.packed;
+        }
         if ((lane & 3) == 0) q8k.bsums[blk * 16 + lane / 4] = (int16_t)r.quad_sum;
         if (lane == 0) q8k.d[blk] = r.d;
     }

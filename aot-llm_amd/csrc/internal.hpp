@@ -57,6 +57,15 @@ struct ActQ8K {
     int8_t *qs;      // [rows][n]
     float *d;        // [rows][n/256]
     int16_t *bsums;  // [rows][n/16]
+    // Batches: a second copy of the quants in the matrix-core fragment order
+    // (null = none), 4 KB per 16-vector tile and super-block, tiles outer:
+    // [tile][super-block][step pair p][k group g][vector v % 16][16 bytes],
+    // byte 8h + b holding element 32(2p + h) + 8g + b of the super-block, so
+    // that one 16-byte load per lane and step pair gives the A operands of
+    // v_mfma_i32_16x16x32_i8 for 16 vectors (see k_mm_kx).
+    int8_t *qt;
+    int tok;  // vector index of this view's first row
+    int nbt;  // super-blocks per vector (n / 256) of the tiled copy
 };
 struct ActQ8_0 {
     int8_t *qs;     // [rows][n]
@@ -65,8 +74,10 @@ struct ActQ8_0 {
 };
 
 // Bytes of an activation buffer for `rows` vectors of n elements.
+// Batches of 2 or more vectors also hold the tiled copy (whole 16-vector tiles).
 inline size_t act_q8k_bytes(size_t n, size_t rows) {
-    return align_up(rows * n, 256) + align_up(rows * (n / 256) * 4, 256) + align_up(rows * (n / 16) * 2, 256);
+    return align_up(rows * n, 256) + align_up(rows * (n / 256) * 4, 256) + align_up(rows * (n / 16) * 2, 256) +
+           (rows >= 2 ? align_up(align_up(rows, 16) * n, 256) : 0);
 }
 inline ActQ8K act_q8k_view(void *base, size_t n, size_t rows) {
     uint8_t *p = (uint8_t *)base;
@@ -76,7 +87,17 @@ inline ActQ8K act_q8k_view(void *base, size_t n, size_t rows) {
     a.d = (float *)p;
     p += align_up(rows * (n / 256) * 4, 256);
     a.bsums = (int16_t *)p;
+    p += align_up(rows * (n / 16) * 2, 256);
+    a.qt = rows >= 2 ? (int8_t *)p : nullptr;
+    a.tok = 0;
+    a.nbt = (int)(n / 256);
     return a;
+}
+
+// Byte offset in the tiled copy of element e of super-block sb of vector v.
+__host__ __device__ inline size_t q8k_tiled_off(size_t v, int sb, int nbt, int e) {
+    const int j = e >> 5, g = (e >> 3) & 3;
+    return ((v >> 4) * (size_t)nbt + sb) * 4096 + (size_t)((j >> 1) * 1024 + (g * 16 + (int)(v & 15)) * 16 + (j & 1) * 8 + (e & 7));
 }
 inline size_t act_q8_0_bytes(size_t n, size_t rows) {
     return align_up(rows * n, 256) + align_up(rows * (n / 32) * 4, 256) + align_up(rows * n * 2, 256);

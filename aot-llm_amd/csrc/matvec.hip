@@ -41,6 +41,7 @@ struct MvArgs {
     const float *xd;
     const int16_t *xbs;
     const float *xf;
+    const int8_t *xt;  // Q8_K batches: the tiled copy of the quants (ActQ8K::qt)
     uint16_t *xh;  // Q8_0 family, batches: the quants as f16 (written before the matmul)
     // K-quant rows, one token: when set, every block quantizes this f32
     // input to Q8_K itself (instead of reading xq / xd / xbs)
@@ -723,28 +724,29 @@ __device__ __forceinline__ void mm_load(MmW<KIND> &w, const uint8_t *rowp, const
     }
 }
 
-// One super-block of the 16 rows of a wave for its tiles of 16 tokens:
-// the B fragments are unpacked once, then per tile the exact integer dots
-// (v_mfma_i32_16x16x32_i8), the scale products and the f32 term of the
-// matvec fold (matvec.rs:82-167 per token): term_out[t][i] belongs to
-// token 16t + 4q + i of the lane's row. ys: the tiles' activation rows of
-// this super-block (MM_YS bytes per token); yds: their Q8_K scales.
-template <int KIND, int TT>
-__device__ __forceinline__ void mm_sb_terms(const MmW<KIND> &cur, const uint8_t *ys, const float *yds, int q, int r16,
-                                            int mt, float (&term_out)[TT][4]) {
-    // the lane row's scales (and mins) of this super-block
-    int sc[16], mn[8];
+// The B side of one super-block of the 16 rows of a wave, unpacked once and
+// shared by every token tile: the lane's 8 quant values of each 32-value
+// step j (k = 32j + 8q .. +8, as signed int8; Q6_K with the -32 offset
+// applied), the row's scales and, for Q4_K/Q5_K, the mins broadcast to the
+// 8 values of a step.
+template <int KIND>
+struct MmB {
+    long bq[8];
+    int sc[16];
+    int mn[8];
+    float dd, dm;
+};
+
+template <int KIND>
+__device__ __forceinline__ void mm_prep(const MmW<KIND> &cur, MmB<KIND> &b) {
     if (KIND == AOTK_Q6_K) {
         const uint32_t scw[4] = {cur.hdr.x, cur.hdr.y, cur.hdr.z, cur.hdr.w};
 #pragma unroll
-        for (int g = 0; g < 16; g++) sc[g] = (int)(int8_t)((scw[g >> 2] >> (8 * (g & 3))) & 0xFFu);
+        for (int g = 0; g < 16; g++) b.sc[g] = (int)(int8_t)((scw[g >> 2] >> (8 * (g & 3))) & 0xFFu);
     } else {
 #pragma unroll
-        for (int j = 0; j < 8; j++) scale_min_k4(j, cur.hdr.y, cur.hdr.z, cur.hdr.w, sc[j], mn[j]);
+        for (int j = 0; j < 8; j++) scale_min_k4(j, cur.hdr.y, cur.hdr.z, cur.hdr.w, b.sc[j], b.mn[j]);
     }
-    // B fragments (the lane's 8 values of each 32-value step j), shared
-    // by the block's token tiles
-    long bq[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         uint32_t w0, w1;
@@ -771,57 +773,74 @@ __device__ __forceinline__ void mm_sb_terms(const MmW<KIND> &cur, const uint8_t 
                 w1 |= ((hb.y >> j) & 0x01010101u) << 4;
             }
         }
-        bq[j] = (long)(((unsigned long)w1 << 32) | w0);
+        b.bq[j] = (long)(((unsigned long)w1 << 32) | w0);
     }
-    long mb[8];
-    if (KIND != AOTK_Q6_K)
-#pragma unroll
-        for (int j = 0; j < 8; j++) mb[j] = (long)(0x0101010101010101ULL * (unsigned long)mn[j]);
-    float dd = 0.0f, dm = 0.0f;
     if (KIND == AOTK_Q6_K) {
-        dd = cur.d6;
+        b.dd = cur.d6;
+        b.dm = 0.0f;
     } else {
-        dd = f16_to_f32(cur.hdr.x & 0xFFFFu);
-        dm = f16_to_f32(cur.hdr.x >> 16);
+        b.dd = f16_to_f32(cur.hdr.x & 0xFFFFu);
+        b.dm = f16_to_f32(cur.hdr.x >> 16);
     }
+}
+
+// One 16-token tile of a prepared super-block: exact integer dots
+// (v_mfma_i32_16x16x32_i8, A = the tile's activation fragments av[j] =
+// token r16's values k = 32j + 8q .. +8), the scale products and the f32
+// term of the matvec fold (matvec.rs:82-167 per token): term[i] belongs to
+// token 4q + i of the tile and the lane's row; yd[i] is that token's Q8_K d.
+template <int KIND>
+__device__ __forceinline__ void mm_tile(const MmB<KIND> &b, const long (&av)[8], const float (&yd)[4], int q,
+                                        float (&term)[4]) {
+    int sumi[4] = {0, 0, 0, 0};
+    mm_v4i csum = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        if (KIND == AOTK_Q6_K) {
+            // two 16-value scale groups per step: lanes q < 2 hold group 2j, q >= 2 group 2j+1
+            const long b_lo = q < 2 ? b.bq[j] : 0, b_hi = q < 2 ? 0 : b.bq[j];
+            mm_v4i c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
+            c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[j], b_lo, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[j], b_hi, c1, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) sumi[i] += __mul24(b.sc[2 * j], c0[i]) + __mul24(b.sc[2 * j + 1], c1[i]);
+        } else {
+            mm_v4i c = {0, 0, 0, 0};
+            c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[j], b.bq[j], c, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) sumi[i] += __mul24(b.sc[j], c[i]);
+            const long mb = (long)(0x0101010101010101ULL * (unsigned long)b.mn[j]);
+            csum = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[j], mb, csum, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (KIND == AOTK_Q6_K) {
+            term[i] = (b.dd * yd[i]) * (float)sumi[i];
+        } else {
+            term[i] = (b.dd * yd[i]) * (float)sumi[i] - (b.dm * yd[i]) * (float)csum[i];
+        }
+    }
+}
+
+// One super-block of the 16 rows of a wave for its tiles of 16 tokens, the
+// activations staged in LDS: ys holds the tiles' activation rows of this
+// super-block (MM_YS bytes per token), yds their Q8_K scales; term_out[t][i]
+// belongs to token 16t + 4q + i of the lane's row.
+template <int KIND, int TT>
+__device__ __forceinline__ void mm_sb_terms(const MmW<KIND> &cur, const uint8_t *ys, const float *yds, int q, int r16,
+                                            int mt, float (&term_out)[TT][4]) {
+    MmB<KIND> b;
+    mm_prep<KIND>(cur, b);
 #pragma unroll
     for (int t = 0; t < TT; t++) {
         if (16 * t >= mt) break;
-        // A fragments: token 16t + r16, k = 32j + 8q .. +8
         const uint8_t *yrow = ys + (16 * t + r16) * MM_YS + 8 * q;
-        int sumi[4] = {0, 0, 0, 0};
-        mm_v4i csum = {0, 0, 0, 0};
+        long av[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const long av = *(const long *)(yrow + 32 * j);
-            if (KIND == AOTK_Q6_K) {
-                // two 16-value scale groups per step: lanes q < 2 hold group 2j, q >= 2 group 2j+1
-                const long b_lo = q < 2 ? bq[j] : 0, b_hi = q < 2 ? 0 : bq[j];
-                mm_v4i c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
-                c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b_lo, c0, 0, 0, 0);
-                c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b_hi, c1, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; i++) sumi[i] += __mul24(sc[2 * j], c0[i]) + __mul24(sc[2 * j + 1], c1[i]);
-            } else {
-                mm_v4i c = {0, 0, 0, 0};
-                c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bq[j], c, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; i++) sumi[i] += __mul24(sc[j], c[i]);
-                csum = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, mb[j], csum, 0, 0, 0);
-            }
-        }
-        // the terms of tokens 16t + 4q + i of the lane's row
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float yd = yds[16 * t + 4 * q + i];
-            float term;
-            if (KIND == AOTK_Q6_K) {
-                term = (dd * yd) * (float)sumi[i];
-            } else {
-                term = (dd * yd) * (float)sumi[i] - (dm * yd) * (float)csum[i];
-            }
-            term_out[t][i] = term;
-        }
+        for (int j = 0; j < 8; j++) av[j] = *(const long *)(yrow + 32 * j);
+        const float yd[4] = {yds[16 * t + 4 * q], yds[16 * t + 4 * q + 1], yds[16 * t + 4 * q + 2], yds[16 * t + 4 * q + 3]};
+        mm_tile<KIND>(b, av, yd, q, term_out[t]);
     }
 }
 
@@ -1013,95 +1032,170 @@ __global__ __launch_bounds__(256) void k_mm_ks(MvArgs a, int m) {
     }
 }
 
-// Prompt matmul, all tokens (m <= 64) in one block of 16 weight rows: the
-// 4 waves split the super-blocks (wave w: w, w + 4, ...) and each runs all
-// the token tiles of its super-block in turn, so a super-block's B
-// fragments are unpacked once for up to 64 tokens (mm_sb_terms per tile on
-// the same weights: the unpacking is common to the calls and computed
-// once). A tile's activation (16 tokens x 256 bytes) is staged in the
-// wave's LDS, the next tile's (or the next super-block's first) loads in
-// flight meanwhile. Per round the four super-blocks' terms meet in LDS and
-// wave t adds those of tile t in super-block order (the matvec fold).
+// Prompt matmul, all tokens (m <= 64) of 16 weight rows per block, the
+// super-blocks split over the block's W waves (wave w: w, w + W, ...). The
+// activation operands come straight from global memory in the tiled order of
+// ActQ8K::qt (16-byte loads, 1 KB contiguous per wave load; the batch stays
+// in L2), all token tiles of a super-block issued at once, and the wave's
+// next super-block's weights are loaded a whole super-block ahead; the Q8_K
+// scales of the batch are staged once per block in LDS, transposed to
+// [super-block][token]. Per round of W super-blocks each wave leaves its
+// terms in LDS and wave t (t < tiles) adds those of token tile t in
+// super-block order, so every output is the matvec's fold (bit-identical to
+// m matvecs). Tokens past m in the last tile compute on whatever the tiled
+// copy holds there (matrix-core rows are independent) and are not stored.
+constexpr int MMX_MAX_NB = 64;
+
+// A operands of token tiles t0, t0 + 1 of super-block sb from the tiled
+// copy: lane l's 16 bytes of step pair p at p*1024 + 16l.
+__device__ __forceinline__ void mmx_load2(uint4 (&at)[2][4], const int8_t *xt, int sb, int t0, int ntiles,
+                                          size_t tile_stride, int lane) {
+    const uint8_t *ab = (const uint8_t *)xt + (size_t)sb * 4096 + 16 * lane;
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int t = min(t0 + u, ntiles - 1);  // past the batch: the last tile again (never folded)
+#pragma unroll
+        for (int p = 0; p < 4; p++) at[u][p] = *(const uint4 *)(ab + t * tile_stride + p * 1024);
+    }
+}
+
+// Terms of two token tiles at once (their matrix-core chains interleaved,
+// no branches between them) into the wave's LDS slot: the same arithmetic
+// as mm_tile per tile. Tiles at or past the batch's last compute on the last
+// tile's operands and are never folded.
 template <int KIND>
-__global__ __launch_bounds__(256) void k_mm_kt(MvArgs a, int m) {
-    __shared__ __align__(16) uint8_t sY[4][2][16 * MM_YS];
-    __shared__ float sD[4][2][16];
-    __shared__ float sT[4][4][4][64];  // [slot][tile][i][lane]
+__device__ __forceinline__ void mmx_tiles2(const MmB<KIND> &b, const uint4 (&at)[2][4], const float *sD, int sb, int t0,
+                                           int q, int lane, float (*slot)[64][4]) {
+    long av[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            av[u][2 * p] = (long)(((unsigned long)at[u][p].y << 32) | at[u][p].x);
+            av[u][2 * p + 1] = (long)(((unsigned long)at[u][p].w << 32) | at[u][p].z);
+        }
+    int sumi[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+    mm_v4i csum[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        if (KIND == AOTK_Q6_K) {
+            const long b_lo = q < 2 ? b.bq[j] : 0, b_hi = q < 2 ? 0 : b.bq[j];
+            mm_v4i c0[2], c1[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const mm_v4i z = {0, 0, 0, 0};
+                c0[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[u][j], b_lo, z, 0, 0, 0);
+                c1[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[u][j], b_hi, z, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) sumi[u][i] += __mul24(b.sc[2 * j], c0[u][i]) + __mul24(b.sc[2 * j + 1], c1[u][i]);
+        } else {
+            const long mb = (long)(0x0101010101010101ULL * (unsigned long)b.mn[j]);
+            mm_v4i c[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const mm_v4i z = {0, 0, 0, 0};
+                c[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[u][j], b.bq[j], z, 0, 0, 0);
+                csum[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[u][j], mb, csum[u], 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) sumi[u][i] += __mul24(b.sc[j], c[u][i]);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const float4 y4 = *(const float4 *)&sD[sb * 64 + 16 * (t0 + u) + 4 * q];
+        const float yd[4] = {y4.x, y4.y, y4.z, y4.w};
+        float term[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (KIND == AOTK_Q6_K) term[i] = (b.dd * yd[i]) * (float)sumi[u][i];
+            else term[i] = (b.dd * yd[i]) * (float)sumi[u][i] - (b.dm * yd[i]) * (float)csum[u][i];
+        }
+        *(float4 *)slot[t0 + u][lane] = make_float4(term[0], term[1], term[2], term[3]);
+    }
+}
+
+template <int KIND, int W>
+__global__ __launch_bounds__(64 * W) void k_mm_kx(MvArgs a, int m) {
+    __shared__ __align__(16) float sD[MMX_MAX_NB * 64];    // [super-block][token]
+    __shared__ __align__(16) float sT[2][W][4][64][4];     // [round parity][slot][tile][lane][i]
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane >> 4, r16 = lane & 15;
     const int nb = a.nb;
-    const int grow = blockIdx.x * 16 + r16;
     const int mt = min(64, m);
     const int ntiles = (mt + 15) / 16;
-    const bool row_ok = grow < a.total_rows;
-    int local;
-    const int sg = seg_of(a, row_ok ? grow : 0, local);
-    const uint8_t *rowp = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * nb * KqGeom<KIND>::RB;
-    const uint16_t *drow = KIND == AOTK_Q6_K ? (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb : nullptr;
-    struct Stg {
-        uint4 v[4];  // 16 tokens x 16 uint4
-        float d;
+    const int ngroups = (a.total_rows + 15) / 16;
+    const int rounds = (nb + W - 1) / W;
+    const size_t tile_stride = (size_t)nb * 4096;
+    for (int idx = threadIdx.x; idx < mt * nb; idx += 64 * W) {
+        const int tk = idx / nb, sb = idx - tk * nb;
+        sD[sb * 64 + tk] = a.xd[idx];
+    }
+    // the wave's items: (row group g, super-block sb), groups strided by the grid
+    auto rows_of = [&](int g, const uint8_t *&rowp, const uint16_t *&drow) {
+        const int grow = g * 16 + r16;
+        int local;
+        const int sg = seg_of(a, grow < a.total_rows ? grow : 0, local);
+        rowp = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * nb * KqGeom<KIND>::RB;
+        drow = KIND == AOTK_Q6_K ? (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb : nullptr;
     };
-    auto stage_load = [&](Stg &r, int sb, int t) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int idx = lane + 64 * k;
-            const int tk = 16 * t + (idx >> 4), c = idx & 15;
-            r.v[k] = tk < mt ? *(const uint4 *)(a.xq + (size_t)tk * a.cols + (size_t)sb * 256 + 16 * c) : make_uint4(0, 0, 0, 0);
-        }
-        const int tk = 16 * t + lane;
-        r.d = lane < 16 && tk < mt ? a.xd[(size_t)tk * nb + sb] : 0.0f;
-    };
-    auto stage_store = [&](const Stg &r, int buf) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int idx = lane + 64 * k;
-            *(uint4 *)(sY[wave][buf] + (idx >> 4) * MM_YS + 16 * (idx & 15)) = r.v[k];
-        }
-        if (lane < 16) sD[wave][buf][lane] = r.d;
-    };
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // waves < ntiles: tile `wave`
-    const int rounds = (nb + 3) / 4;
+    const uint8_t *rowp, *rown;
+    const uint16_t *drow, *drown;
+    int g = blockIdx.x;
+    rows_of(g, rowp, drow);
     MmW<KIND> cur, nxt;
-    Stg st;
-    if (wave < nb) {
-        mm_load<KIND>(cur, rowp, drow, wave, nb, q);
-        stage_load(st, wave, 0);
-    }
-    for (int r = 0; r < rounds; r++) {
-        const int sb = 4 * r + wave;
-        if (sb < nb) {
-            if (sb + 4 < nb) mm_load<KIND>(nxt, rowp, drow, sb + 4, nb, q);
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                if (t >= ntiles) break;
-                stage_store(st, t & 1);
-                wave_lds_sync();
-                if (t + 1 < ntiles) stage_load(st, sb, t + 1);
-                else if (sb + 4 < nb) stage_load(st, sb + 4, 0);
-                float term[1][4];
-                mm_sb_terms<KIND, 1>(cur, sY[wave][t & 1], sD[wave][t & 1], q, r16, mt - 16 * t, term);
-#pragma unroll
-                for (int i = 0; i < 4; i++) sT[wave][t][i][lane] = term[0][i];
+    if (wave < nb) mm_load<KIND>(cur, rowp, drow, wave, nb, q);
+    __syncthreads();
+    int par = 0;
+    for (; g < ngroups; g += gridDim.x) {
+        const int gn = g + gridDim.x;
+        if (gn < ngroups) rows_of(gn, rown, drown);
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // waves < ntiles: tile `wave`
+        for (int r = 0; r < rounds; r++, par ^= 1) {
+            const int sb = r * W + wave;
+            if (sb < nb) {
+                // the next item's weights: the next round of this group, or the first of the next group
+                if (sb + W < nb) mm_load<KIND>(nxt, rowp, drow, sb + W, nb, q);
+                else if (gn < ngroups) mm_load<KIND>(nxt, rown, drown, wave, nb, q);
+                MmB<KIND> b;
+                mm_prep<KIND>(cur, b);
+                uint4 at[2][4];
+                mmx_load2(at, a.xt, sb, 0, ntiles, tile_stride, lane);
+                mmx_tiles2<KIND>(b, at, sD, sb, 0, q, lane, sT[par][wave]);
+                if (ntiles > 2) {
+                    mmx_load2(at, a.xt, sb, 2, ntiles, tile_stride, lane);
+                    mmx_tiles2<KIND>(b, at, sD, sb, 2, q, lane, sT[par][wave]);
+                }
+                cur = nxt;
             }
-            if (sb + 4 < nb) cur = nxt;
+            __syncthreads();
+            if (wave < ntiles) {
+                const int n = min(W, nb - r * W);
+                for (int slot = 0; slot < n; slot++) {
+                    const float4 v = *(const float4 *)sT[par][slot][wave][lane];
+                    acc[0] = acc[0] + v.x;
+                    acc[1] = acc[1] + v.y;
+                    acc[2] = acc[2] + v.z;
+                    acc[3] = acc[3] + v.w;
+                }
+            }
         }
-        __syncthreads();
-        if (wave < ntiles) {
-            const int n = min(4, nb - 4 * r);
-            for (int slot = 0; slot < n; slot++)
+        const int grow = g * 16 + r16;
+        if (wave < ntiles && grow < a.total_rows) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[i] = acc[i] + sT[slot][wave][i][lane];
+            for (int i = 0; i < 4; i++) {
+                const int tk = 16 * wave + 4 * q + i;
+                if (tk < mt) store_row(a, grow, tk, acc[i]);
+            }
         }
-        __syncthreads();
-    }
-    if (wave < ntiles && row_ok) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int tk = 16 * wave + 4 * q + i;
-            if (tk < mt) store_row(a, grow, tk, acc[i]);
-        }
+        rowp = rown;
+        drow = drown;
     }
 }
 
@@ -1954,6 +2048,7 @@ static MvArgs make_args(int n, const DevWeight *const ws[], float *const ys[], c
         a.xq = q.qs;
         a.xd = q.d;
         a.xbs = q.bsums;
+        a.xt = q.qt;
     } else if (act == ACT_Q8_0) {
         ActQ8_0 q = *(const ActQ8_0 *)x_act;
         a.xq = q.qs;
@@ -2025,6 +2120,22 @@ static void launch_kq(const MvArgs &a, dim3 grid, hipStream_t s) {
     }
 }
 
+// Persistent k_mm_kx: one round of resident blocks (the occupancy of the
+// instance on this device, queried once) walks the 16-row groups.
+template <int KIND, int W>
+static void launch_mm_kx(const MvArgs &a, int m, hipStream_t s) {
+    static int resident = 0;
+    if (!resident) {
+        int dev = 0, cus = 0, per = 0;
+        (void)hipGetDevice(&dev);
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_mm_kx<KIND, W>, 64 * W, 0);
+        resident = std::max(1, cus) * std::max(1, per);
+    }
+    const int groups = (a.total_rows + 15) / 16;
+    k_mm_kx<KIND, W><<<dim3((unsigned)std::min(groups, resident)), 64 * W, 0, s>>>(a, m);
+}
+
 static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
     dim3 grid;
     grid.y = (unsigned)m;
@@ -2037,17 +2148,17 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
         // Q6_K down slightly faster, 4096-row Q4_K wo slightly slower):
         // super-blocks split over the waves
         const unsigned cells = rb * (unsigned)tiles;
-        // 2048 rows or more: the whole batch per 16-row block, super-blocks
-        // split over the waves (measured at 64 tokens: the 4096-row Q6_K
-        // down 82 -> 69 us, the 4096/5120-row Q4_K wo and q/k 20/24 -> 19/22
-        // us, the 28672-row gate/up unchanged); fewer rows leave too few
-        // blocks (the 1024-row v: 12 -> 21 us) and keep the kernels below
-        if (a.total_rows >= 2048) {
-            dim3 gk((unsigned)((a.total_rows + 15) / 16), 1);
+        // 2048 rows or more with the tiled input: k_mm_kx (measured at 64
+        // tokens against the LDS-staged k_mm_kq family: the 4096-row Q4_K
+        // wo 16.0 -> 10.4 us, the 28672-row gate/up 73 -> 50 us, the
+        // 4096-row Q6_K down 61 -> 41 us; blocks of 4 waves for the tallest
+        // Q4_K/Q5_K matrices, of 8 otherwise)
+        if (a.total_rows >= 2048 && a.nb <= MMX_MAX_NB && a.xt) {
+            const bool tall = a.total_rows >= 16384;
             switch (kind) {
-            case AOTK_Q4_K: k_mm_kt<AOTK_Q4_K><<<gk, 256, 0, s>>>(a, (int)m); break;
-            case AOTK_Q5_K: k_mm_kt<AOTK_Q5_K><<<gk, 256, 0, s>>>(a, (int)m); break;
-            default: k_mm_kt<AOTK_Q6_K><<<gk, 256, 0, s>>>(a, (int)m); break;
+            case AOTK_Q4_K: tall ? launch_mm_kx<AOTK_Q4_K, 4>(a, (int)m, s) : launch_mm_kx<AOTK_Q4_K, 8>(a, (int)m, s); break;
+            case AOTK_Q5_K: tall ? launch_mm_kx<AOTK_Q5_K, 4>(a, (int)m, s) : launch_mm_kx<AOTK_Q5_K, 8>(a, (int)m, s); break;
+            default: launch_mm_kx<AOTK_Q6_K, 8>(a, (int)m, s); break;
             }
             return;
         }

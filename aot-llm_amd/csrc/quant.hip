@@ -362,8 +362,10 @@ __global__ void k_quant_q8k(const float *__restrict__ x, size_t nblk, ActQ8K out
         if (oa > amax || (oa == amax && oi < idx)) { amax = oa; idx = oi; }
     }
     int8_t *qs = out.qs + blk * 256;
+    uint32_t *qt = out.qt ? (uint32_t *)(out.qt + q8k_tiled_off(blk / out.nbt, (int)(blk % out.nbt), out.nbt, 4 * lane)) : nullptr;
     if (amax == 0.0f) {
         ((uint32_t *)qs)[lane] = 0;
+        if (qt) *qt = 0;
         if ((lane & 3) == 0) out.bsums[blk * 16 + lane / 4] = 0;
         if (lane == 0) out.d[blk] = 0.0f;
         return;
@@ -377,8 +379,10 @@ __global__ void k_quant_q8k(const float *__restrict__ x, size_t nblk, ActQ8K out
         q[k] = t > 127 ? 127 : t;
         sum += (int8_t)q[k];
     }
-    ((uint32_t *)qs)[lane] = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) |
-                             ((uint32_t)(q[3] & 0xFF) << 24);
+    const uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) |
+                            ((uint32_t)(q[3] & 0xFF) << 24);
+    ((uint32_t *)qs)[lane] = packed;
+    if (qt) *qt = packed;
     sum += shfl_xor(sum, 1);
     sum += shfl_xor(sum, 2);
     if ((lane & 3) == 0) out.bsums[blk * 16 + lane / 4] = (int16_t)sum;
@@ -402,6 +406,8 @@ __global__ void k_quant_q8_0(const float *__restrict__ x, size_t nblk, ActQ8_0 o
 
 void launch_quant_q8k(const float *x, size_t n, size_t rows, ActQ8K out, hipStream_t s) {
     size_t nblk = rows * n / 256;
+    out.nbt = (int)(n / 256);
+    if (rows < 2) out.qt = nullptr;
     k_quant_q8k<<<(unsigned)((nblk + 3) / 4), 256, 0, s>>>(x, nblk, out);
 }
 
@@ -426,6 +432,7 @@ __global__ void k_ref_to_q8k(const aotk_block_q8_k *in, size_t nblk, ActQ8K a) {
     size_t b = i / 256;
     int e = (int)(i % 256);
     a.qs[i] = in[b].qs[e];
+    if (a.qt) a.qt[q8k_tiled_off(b / a.nbt, (int)(b % a.nbt), a.nbt, e)] = in[b].qs[e];
     if (e < 16) a.bsums[b * 16 + e] = in[b].bsums[e];
     if (e == 0) a.d[b] = in[b].d;
 }
@@ -452,6 +459,8 @@ void launch_q8k_to_ref(ActQ8K a, size_t n, aotk_block_q8_k *out, hipStream_t s) 
 }
 void launch_ref_to_q8k(const aotk_block_q8_k *in, size_t n, size_t rows, ActQ8K a, hipStream_t s) {
     size_t nblk = rows * n / 256;
+    a.nbt = (int)(n / 256);
+    if (rows < 2) a.qt = nullptr;
     k_ref_to_q8k<<<(unsigned)((nblk * 256 + 255) / 256), 256, 0, s>>>(in, nblk, a);
 }
 void launch_q8_0_to_ref(ActQ8_0 a, size_t n, aotk_block_q8_0 *out, hipStream_t s) {

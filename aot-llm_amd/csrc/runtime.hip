@@ -1450,35 +1450,36 @@ int aotk_prefix_load(aotk_state *st, const void *blob, size_t len, uint32_t *tok
 
 extern "C" {
 
-int aotk_time_matvec(const aotk_weight *const *ws, size_t n_w, const float *x_dev, size_t iters, float *ms_per_launch) {
+int aotk_time_matmul(const aotk_weight *const *ws, size_t n_w, const float *xs_dev, size_t m, size_t iters,
+                     float *ms_per_launch) {
     if (ensure_init()) return -1;
-    if (!ws || n_w == 0 || iters == 0) return fail("time_matvec: nothing to time");
+    if (!ws || n_w == 0 || iters == 0 || m == 0) return fail("time_matmul: nothing to time");
     const DevWeight &w0 = ws[0]->dw;
     for (size_t i = 1; i < n_w; i++)
         if (ws[i]->dw.kind != w0.kind || ws[i]->dw.cols != w0.cols || ws[i]->dw.rows != w0.rows)
-            return fail("time_matvec: weights differ in kind or shape");
+            return fail("time_matmul: weights differ in kind or shape");
     int a = activation(w0.kind);
-    size_t act_bytes = a == ACT_Q8_K ? act_q8k_bytes(w0.cols, 1) : (a == ACT_Q8_0 ? act_q8_0_bytes(w0.cols, 1) : 0);
-    void *s = lib_scratch(act_bytes + align_up(w0.rows * 4, 256));
+    size_t act_bytes = a == ACT_Q8_K ? act_q8k_bytes(w0.cols, m) : (a == ACT_Q8_0 ? act_q8_0_bytes(w0.cols, m) : 0);
+    void *s = lib_scratch(act_bytes + align_up(m * w0.rows * 4, 256));
     if (!s) return -1;
     float *y = (float *)((uint8_t *)s + act_bytes);
     ActQ8K qk;
     ActQ8_0 q0;
-    const void *act = x_dev;
+    const void *act = xs_dev;
     if (a == ACT_Q8_K) {
-        qk = act_q8k_view(s, w0.cols, 1);
-        launch_quant_q8k(x_dev, w0.cols, 1, qk, g_stream);
+        qk = act_q8k_view(s, w0.cols, m);
+        launch_quant_q8k(xs_dev, w0.cols, m, qk, g_stream);
         act = &qk;
     } else if (a == ACT_Q8_0) {
-        q0 = act_q8_0_view(s, w0.cols, 1);
-        launch_quant_q8_0(x_dev, w0.cols, 1, q0, g_stream);
+        q0 = act_q8_0_view(s, w0.cols, m);
+        launch_quant_q8_0(xs_dev, w0.cols, m, q0, g_stream);
         act = &q0;
     }
     hipEvent_t e0, e1;
     HIPC(hipEventCreate(&e0));
     HIPC(hipEventCreate(&e1));
     HIPC(hipEventRecord(e0, g_stream));
-    for (size_t it = 0; it < iters; it++) launch_matvec(ws[it % n_w]->dw, act, 1, y, nullptr, g_stream);
+    for (size_t it = 0; it < iters; it++) launch_matvec(ws[it % n_w]->dw, act, m, y, nullptr, g_stream);
     HIPC(hipEventRecord(e1, g_stream));
     HIPC(hipEventSynchronize(e1));
     float ms = 0.0f;
@@ -1488,6 +1489,10 @@ int aotk_time_matvec(const aotk_weight *const *ws, size_t n_w, const float *x_de
     HIPC(hipGetLastError());
     *ms_per_launch = ms / (float)iters;
     return 0;
+}
+
+int aotk_time_matvec(const aotk_weight *const *ws, size_t n_w, const float *x_dev, size_t iters, float *ms_per_launch) {
+    return aotk_time_matmul(ws, n_w, x_dev, 1, iters, ms_per_launch);
 }
 
 }  // extern "C"

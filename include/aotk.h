@@ -213,8 +213,9 @@ int aotk_matmul2(const aotk_weight *w_a, const aotk_weight *w_b, const void *xs_
  * tight serving loops, harnesses that forbid hipMalloc). The Q8_0 / Q8_K
  * inputs are staged in a fixed 4 MiB device array of the library (one per
  * GPU, held until the process ends) instead of the growable scratch; calls
- * whose staging needs more (m * cols * ~1.14 bytes for Q8_K, ~1.13 for Q8_0,
- * e.g. m = 64 at cols up to 28672) fail with -1. Results equal aotk_matmul's
+ * whose staging needs more (m * cols * ~2.14 bytes for Q8_K batches of 2 or
+ * more, ~1.14 for one input, ~3.13 for Q8_0, e.g. m = 64 at cols up to
+ * 28672 for Q8_K) fail with -1. Results equal aotk_matmul's
  * bit for bit. Every call on a GPU shares that GPU's array: calls that
  * overlap on one GPU (from several threads) race. */
 int aotk_matmul_noalloc(const aotk_weight *w, const void *xs_dev, size_t m, float *out_dev);
@@ -348,6 +349,12 @@ int aotk_prefix_load(aotk_state *state, const void *blob, size_t len, uint32_t *
  * the working set out of the 256 MB Infinity Cache) `iters` times on the
  * library stream, timed with HIP events; writes the mean ms per launch. */
 int aotk_time_matvec(const aotk_weight *const *ws, size_t n_w, const float *x_dev, size_t iters, float *ms_per_launch);
+
+/* aotk_time_matvec for a batch: m input vectors of cols floats back to back
+ * in xs_dev, quantized once, then the batched product (the prompt kernels
+ * for m >= 2) launched `iters` times over ws[0], ws[1], ... in turn. */
+int aotk_time_matmul(const aotk_weight *const *ws, size_t n_w, const float *xs_dev, size_t m, size_t iters,
+                     float *ms_per_launch);
 
 /* The library's HIP stream (hipStream_t) for callers that time on it. */
 void *aotk_stream(void);
