@@ -518,6 +518,107 @@ __global__ __launch_bounds__(512) void k_attn_scores_rb(AttnArgs a, int m) {
             a.prob[((size_t)(i0 + r) * a.n_head + (size_t)(kvh * gqa + hg)) * a.span + (t - t0[r])] = sc[r] * a.scale;
 }
 
+// Wave-uniform operands through the scalar unit: loads through a pointer in
+// the constant address space become s_load (the data is not written during
+// the kernel), so a value every lane needs costs no vector load or LDS read.
+typedef const float __attribute__((address_space(4))) *att_cfp;
+typedef float att_f8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ att_f8 att_sload8(const float *p) { return *(const __attribute__((address_space(4))) att_f8 *)p; }
+
+
+// Prompt scores: block = (kv head, chunk of 64 absolute positions, group of
+// R rows), GQA waves; thread (query head hg = wave, position = lane) runs the
+// R rows' dot products side by side, each sequentially over the head
+// dimension (s += q[d] * k[d], ops.rs:160-166), then scales them. The q
+// values are wave-uniform: scalar loads, 8 dimensions of the R rows at a
+// time. The chunk's K rows are staged in LDS 32 dimensions at a time (one
+// 16-byte read per lane and 4 dimensions), the next 32 in flight.
+constexpr int ATT_KD = 32;  // dimensions per K stage
+template <int HD, int GQA, int R>
+__global__ __launch_bounds__(64 * GQA) void k_attn_scores_sg(AttnArgs a, int m) {
+    constexpr int KS = ATT_KD + 4;
+    constexpr int NT = 64 * GQA;
+    constexpr int NL = 64 * ATT_KD / 4 / NT;  // float4 loads per thread and stage
+    static_assert(NL >= 1, "stage");
+    __shared__ __align__(16) float sk[2][64][KS];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int hg = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kvh = blockIdx.x;
+    const size_t start = (size_t)blockIdx.y * 64;
+    const int i0 = blockIdx.z * R;
+    size_t t0[R], tn[R];
+    size_t lo = ~(size_t)0, hi = 0;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        row_range(a, (size_t)min(i0 + r, m - 1), t0[r], tn[r]);
+        if (i0 + r >= m) tn[r] = t0[r];  // rows past m: empty
+        lo = min(lo, t0[r]);
+        hi = max(hi, tn[r]);
+    }
+    if (start >= hi || start + 64 <= lo) return;  // no row has a position here
+    const size_t kv = (size_t)a.n_kv_head * HD, q_dim = (size_t)a.n_head * HD;
+    const float *qr[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) qr[r] = a.q + (size_t)min(i0 + r, m - 1) * q_dim + (size_t)(kvh * GQA + hg) * HD;
+    // stage loads: position c / (ATT_KD / 4), dims 4 (c % (ATT_KD / 4)) of the stage (positions past the
+    // union's end re-read its last one)
+    const float *kb = a.k_cache + (size_t)kvh * HD;
+    float4 lk[NL];
+    auto fetch = [&](int dc) {
+#pragma unroll
+        for (int k = 0; k < NL; k++) {
+            const int c = tid + NT * k;
+            const size_t t = min(start + (size_t)(c / (ATT_KD / 4)), hi - 1);
+            lk[k] = *(const float4 *)(kb + t * kv + dc + 4 * (c % (ATT_KD / 4)));
+        }
+    };
+    auto put = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < NL; k++) {
+            const int c = tid + NT * k;
+            *(float4 *)&sk[buf][c / (ATT_KD / 4)][4 * (c % (ATT_KD / 4))] = lk[k];
+        }
+    };
+    fetch(0);
+    put(0);
+    __syncthreads();
+    float sc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) sc[r] = 0.0f;
+    int buf = 0;
+    for (int dc = 0; dc < HD; dc += ATT_KD) {
+        const bool more = dc + ATT_KD < HD;
+        if (more) fetch(dc + ATT_KD);
+#pragma unroll
+        for (int d8 = 0; d8 < ATT_KD; d8 += 8) {
+            att_f8 q8[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) q8[r] = att_sload8(qr[r] + dc + d8);
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const float4 k4 = *(const float4 *)&sk[buf][lane][d8 + 4 * h];
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    sc[r] = sc[r] + q8[r][4 * h] * k4.x;
+                    sc[r] = sc[r] + q8[r][4 * h + 1] * k4.y;
+                    sc[r] = sc[r] + q8[r][4 * h + 2] * k4.z;
+                    sc[r] = sc[r] + q8[r][4 * h + 3] * k4.w;
+                }
+            }
+        }
+        if (more) {
+            put(buf ^ 1);  // the other buffer was last read before the previous barrier
+            __syncthreads();
+            buf ^= 1;
+        }
+    }
+    const size_t t = start + lane;
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        if (t >= t0[r] && t < tn[r])
+            a.prob[((size_t)(i0 + r) * a.n_head + (size_t)(kvh * GQA + hg)) * a.span + (t - t0[r])] = sc[r] * a.scale;
+}
+
 // One wave's share of the q/k/v epilogue for one head vector (decode):
 // bias, rmsnorm_heads (sequential sum of squares by lane 0), rope with the
 // position's table row; the result is left in `hv` (LDS, HD floats). The
@@ -1057,6 +1158,7 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_softmax_rows_x(AttnArgs a, int m
     }
 }
 
+
 static void launch_rows(const AttnArgs &a, size_t head_dim, size_t m, size_t longest, hipStream_t s) {
     const unsigned pairs = (unsigned)(m * a.n_head);
     if (longest <= (size_t)ATT_ROWS_MAX) k_attn_softmax_rows<4, ATT_ROWS_MAX><<<(pairs + 3) / 4, 256, 0, s>>>(a, (int)m);
@@ -1114,7 +1216,21 @@ void launch_attention(float *out, const float *q, const float *k_cache, const fl
     size_t span = window > 0 && window < ctx_rows ? window : ctx_rows;
     dim3 grid((unsigned)n_kv_head, (unsigned)((span + ATT_CH - 1) / ATT_CH), (unsigned)m);
     const unsigned threads = (unsigned)(64 * (n_head / n_kv_head));
-    if (m > 1 && !pos_dev && head_dim <= 128) {
+    if (m > 1 && !pos_dev && head_dim == 256 && n_head / n_kv_head <= 8) {
+        // head_dim 256: rows batched per block, q through the scalar unit
+        // (measured at 64 rows: 8192 positions 839 -> 188 us, a 1024 window
+        // 68 -> 43 us; at head_dim 128 the per-row-group kernel below stays
+        // ahead, 107 against 114 us at 4096 positions)
+        const size_t hi = pos0 + m;  // the last row's end
+        const int gqa = (int)(n_head / n_kv_head);
+        dim3 g4((unsigned)n_kv_head, (unsigned)((hi + 63) / 64), (unsigned)((m + 3) / 4));
+        switch (gqa) {
+        case 1: k_attn_scores_sg<256, 1, 4><<<g4, 64, 0, s>>>(a, (int)m); break;
+        case 2: k_attn_scores_sg<256, 2, 4><<<g4, 128, 0, s>>>(a, (int)m); break;
+        case 4: k_attn_scores_sg<256, 4, 4><<<g4, 256, 0, s>>>(a, (int)m); break;
+        default: k_attn_scores_sg<256, 8, 4><<<g4, 512, 0, s>>>(a, (int)m); break;
+        }
+    } else if (m > 1 && !pos_dev && head_dim <= 128) {
         // several rows per block over absolute position chunks
         const size_t hi = pos0 + m;  // the last row's end
         dim3 g((unsigned)n_kv_head, (unsigned)((hi + ATT_CH - 1) / ATT_CH), (unsigned)((m + ATT_SRB - 1) / ATT_SRB));
