@@ -1687,8 +1687,8 @@ __device__ __forceinline__ float hsum8(const float (&c)[8]) {
 // Wave = SETS sets of 4 rows x TILES tiles of 16 tokens; block = 4 waves
 // over BR rows x 64 tokens. The activations arrive as f16 (k_q8_to_f16,
 // once per batch), the weights are converted to f16 when staged; both are
-// staged in LDS, MQ_BS blocks per stage, two stages in LDS and two more in
-// registers in flight.
+// staged in LDS, BS blocks per stage (2 or 4 by the matrix height), two
+// stages in LDS and two more in registers in flight.
 constexpr int MQ_BS = 2;   // blocks of 32 per stage
 constexpr int MQ_XS = 40;  // halves per (block, token) line of the activation tile (32 + pad)
 
@@ -1719,19 +1719,21 @@ __global__ __launch_bounds__(256) void k_q8_to_f16(const int8_t *__restrict__ xq
     ((u32x4_t *)xh)[2 * i + 1] = u32x4_t{h[4], h[5], h[6], h[7]};
 }
 
-template <int KIND, int SETS, int TILES>
+template <int KIND, int SETS, int TILES, int BS = MQ_BS>
 __global__ __launch_bounds__(256) void k_mm_q8(MvArgs a, int m) {
     constexpr int WTW = 4 / TILES;      // waves along the tokens
     constexpr int WRW = 4 / WTW;        // waves along the rows
     constexpr int BR = WRW * 4 * SETS;  // weight rows per block
     constexpr int QB = KIND == AOTK_Q8_0 ? 32 : 16;  // quant bytes per block
     constexpr int WPT = KIND == AOTK_Q8_0 ? 2 : 1;   // 16-byte quant loads per (row, block)
-    constexpr int WT = BR * MQ_BS * WPT;             // weight staging threads
-    static_assert(WT <= 256, "weight tile");
-    __shared__ __align__(16) _Float16 sx[2][MQ_BS][64][MQ_XS];  // activations
-    __shared__ __align__(16) float sxd[2][MQ_BS][64];           // their scales
-    __shared__ __align__(16) _Float16 sw[2][BR][MQ_BS][32];     // weight quants
-    __shared__ __align__(16) float swd[2][BR][MQ_BS];           // f32(d)
+    constexpr int WT = BR * BS * WPT;                // weight staging loads per stage
+    constexpr int WP = (WT + 255) / 256;             // ... per thread
+    constexpr int YP = (64 * BS + 255) / 256;        // activation scales per thread
+    static_assert((BS & (BS - 1)) == 0, "stage blocks");
+    __shared__ __align__(16) _Float16 sx[2][BS][64][MQ_XS];  // activations
+    __shared__ __align__(16) float sxd[2][BS][64];           // their scales
+    __shared__ __align__(16) _Float16 sw[2][BR][BS][32];     // weight quants
+    __shared__ __align__(16) float swd[2][BR][BS];           // f32(d)
     __shared__ __align__(16) _Float16 szero[8];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1741,58 +1743,75 @@ __global__ __launch_bounds__(256) void k_mm_q8(MvArgs a, int m) {
     const int row0 = blockIdx.x * BR;
     const int mt = min(64, m - t0);
     if (tid < 4) ((uint32_t *)szero)[tid] = 0u;
-    // the weight row / block / 16-byte part this thread stages
-    const int w_part = tid % WPT, w_blk = (tid / WPT) % MQ_BS, w_row = min(tid / (WPT * MQ_BS), BR - 1);
-    const uint8_t *wq;
-    const uint16_t *wd;
-    const uint32_t *wh;
-    {
-        const int grow = min(row0 + w_row, a.total_rows - 1);
+    // the weight rows / blocks / 16-byte parts this thread stages (pass k: c = tid + 256 k)
+    const uint8_t *wq[WP];
+    const uint16_t *wd[WP];
+    const uint32_t *wh[WP];
+#pragma unroll
+    for (int k = 0; k < WP; k++) {
+        const int c = min(tid + 256 * k, WT - 1);
+        const int grow = min(row0 + c / (WPT * BS), a.total_rows - 1);
         int local;
         const int sg = seg_of(a, grow, local);
-        wq = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * nb * QB;
-        wd = (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb;
-        wh = KIND == AOTK_Q5_0 ? (const uint32_t *)seg_sel(sg, a.w2[0], a.w2[1], a.w2[2]) + (size_t)local * nb : nullptr;
+        wq[k] = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * nb * QB;
+        wd[k] = (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb;
+        wh[k] = KIND == AOTK_Q5_0 ? (const uint32_t *)seg_sel(sg, a.w2[0], a.w2[1], a.w2[2]) + (size_t)local * nb : nullptr;
     }
     // stage loads (tokens past m and blocks past the end repeat the last:
     // valid memory, never stored)
     struct Ld {
-        u32x4_t x[2], w;
-        float xd;
-        uint32_t wd, wh;
+        u32x4_t x[BS], w[WP];
+        float xd[YP];
+        uint32_t wd[WP], wh[WP];
     };
     Ld L[2];
     auto fetch = [&](Ld &ld, int c0) {
 #pragma unroll
-        for (int k = 0; k < 2; k++) {  // 64 tokens x 2 blocks x 4 parts of 16 bytes
+        for (int k = 0; k < BS; k++) {  // 64 tokens x BS blocks x 4 parts of 16 bytes
             const int c = tid + 256 * k;
-            const int t = min(t0 + (c >> 3), m - 1), b = min(c0 + ((c >> 2) & 1), nb - 1);
+            const int t = min(t0 + c / (4 * BS), m - 1), b = min(c0 + ((c >> 2) & (BS - 1)), nb - 1);
             ld.x[k] = *(const u32x4_t *)(a.xh + (size_t)t * a.cols + (size_t)b * 32 + (c & 3) * 8);
         }
-        if (tid < 64 * MQ_BS) {
-            const int t = min(t0 + (tid >> 1), m - 1), b = min(c0 + (tid & 1), nb - 1);
-            ld.xd = a.xd[(size_t)t * nb + b];
+#pragma unroll
+        for (int k = 0; k < YP; k++) {
+            const int c = tid + 256 * k;  // (token c / BS, block c % BS)
+            if (c < 64 * BS) {
+                const int t = min(t0 + c / BS, m - 1), b = min(c0 + (c & (BS - 1)), nb - 1);
+                ld.xd[k] = a.xd[(size_t)t * nb + b];
+            }
         }
-        if (tid < WT) {
-            const int b = min(c0 + w_blk, nb - 1);
-            ld.w = *(const u32x4_t *)(wq + (size_t)b * QB + w_part * 16);
-            if (KIND == AOTK_Q5_0) ld.wh = wh[b];
-            if (w_part == 0) ld.wd = wd[b];
+#pragma unroll
+        for (int k = 0; k < WP; k++) {
+            const int c = tid + 256 * k;  // (row c / (WPT BS), block (c / WPT) % BS, part c % WPT)
+            if (c < WT) {
+                const int part = c % WPT, b = min(c0 + (c / WPT) % BS, nb - 1);
+                ld.w[k] = *(const u32x4_t *)(wq[k] + (size_t)b * QB + part * 16);
+                if (KIND == AOTK_Q5_0) ld.wh[k] = wh[k][b];
+                if (part == 0) ld.wd[k] = wd[k][b];
+            }
         }
     };
     auto put = [&](const Ld &ld, int st) {
 #pragma unroll
-        for (int k = 0; k < 2; k++) {
+        for (int k = 0; k < BS; k++) {
             const int c = tid + 256 * k;
-            *(u32x4_t *)&sx[st][(c >> 2) & 1][c >> 3][(c & 3) * 8] = ld.x[k];
+            *(u32x4_t *)&sx[st][(c >> 2) & (BS - 1)][c / (4 * BS)][(c & 3) * 8] = ld.x[k];
         }
-        if (tid < 64 * MQ_BS) sxd[st][tid & 1][tid >> 1] = ld.xd;
-        if (tid < WT) {
-            uint32_t *dst = (uint32_t *)&sw[st][w_row][w_blk][w_part * 16];
+#pragma unroll
+        for (int k = 0; k < YP; k++) {
+            const int c = tid + 256 * k;
+            if (c < 64 * BS) sxd[st][c & (BS - 1)][c / BS] = ld.xd[k];
+        }
+#pragma unroll
+        for (int k = 0; k < WP; k++) {
+            const int c = tid + 256 * k;
+            if (c >= WT) continue;
+            const int part = c % WPT, blk = (c / WPT) % BS, row = c / (WPT * BS);
+            uint32_t *dst = (uint32_t *)&sw[st][row][blk][part * 16];
             if (KIND == AOTK_Q8_0) {
                 uint32_t h[8];
 #pragma unroll
-                for (int i = 0; i < 4; i++) u8x4_to_f16(ld.w[i] ^ 0x80808080u, 128.0f, h[2 * i], h[2 * i + 1]);
+                for (int i = 0; i < 4; i++) u8x4_to_f16(ld.w[k][i] ^ 0x80808080u, 128.0f, h[2 * i], h[2 * i + 1]);
                 *(u32x4_t *)dst = u32x4_t{h[0], h[1], h[2], h[3]};
                 *(u32x4_t *)(dst + 4) = u32x4_t{h[4], h[5], h[6], h[7]};
             } else {
@@ -1800,9 +1819,9 @@ __global__ __launch_bounds__(256) void k_mm_q8(MvArgs a, int m) {
                 uint32_t h[16];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    uint32_t l4 = ld.w[i] & 0x0F0F0F0Fu, h4 = (ld.w[i] >> 4) & 0x0F0F0F0Fu;
+                    uint32_t l4 = ld.w[k][i] & 0x0F0F0F0Fu, h4 = (ld.w[k][i] >> 4) & 0x0F0F0F0Fu;
                     if (KIND == AOTK_Q5_0) {
-                        const uint32_t bl = (ld.wh >> (4 * i)) & 0xFu, bh = (ld.wh >> (16 + 4 * i)) & 0xFu;
+                        const uint32_t bl = (ld.wh[k] >> (4 * i)) & 0xFu, bh = (ld.wh[k] >> (16 + 4 * i)) & 0xFu;
                         l4 |= ((bl & 1u) | ((bl & 2u) << 7) | ((bl & 4u) << 14) | ((bl & 8u) << 21)) << 4;
                         h4 |= ((bh & 1u) | ((bh & 2u) << 7) | ((bh & 4u) << 14) | ((bh & 8u) << 21)) << 4;
                     }
@@ -1813,7 +1832,7 @@ __global__ __launch_bounds__(256) void k_mm_q8(MvArgs a, int m) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) *(u32x4_t *)(dst + 4 * i) = u32x4_t{h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]};
             }
-            if (w_part == 0) swd[st][w_row][w_blk] = f16_to_f32(ld.wd);
+            if (part == 0) swd[st][row][blk] = f16_to_f32(ld.wd[k]);
         }
     };
     // lane roles: q = lane / 16 (the output row in a set of 4, and the
@@ -1828,16 +1847,16 @@ __global__ __launch_bounds__(256) void k_mm_q8(MvArgs a, int m) {
 #pragma unroll
         for (int t = 0; t < TILES; t++) acc[s][t][0] = acc[s][t][1] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
     fetch(L[0], 0);
-    if (MQ_BS < nb) fetch(L[1], MQ_BS);
+    if (BS < nb) fetch(L[1], BS);
     put(L[0], 0);
     __syncthreads();
-    // one stage: stage c0 + 2 * MQ_BS goes into the register set `fr` just
+    // one stage: stage c0 + 2 * BS goes into the register set `fr` just
     // emptied, the stage in `pr` (fetched a round earlier) into the other
     // LDS buffer after the compute (last read in the previous round, before
     // its barrier)
     auto round = [&](int c0, int st, Ld &fr, const Ld &pr) {
-        if (c0 + 2 * MQ_BS < nb) fetch(fr, c0 + 2 * MQ_BS);
-        const int nblk = nb - c0 < MQ_BS ? nb - c0 : MQ_BS;
+        if (c0 + 2 * BS < nb) fetch(fr, c0 + 2 * BS);
+        const int nblk = nb - c0 < BS ? nb - c0 : BS;
         for (int j = 0; j < nblk; j++) {
             h8_t bx[TILES];
             float yd[TILES];
@@ -1869,14 +1888,14 @@ __global__ __launch_bounds__(256) void k_mm_q8(MvArgs a, int m) {
                 }
             }
         }
-        if (c0 + MQ_BS < nb) {
+        if (c0 + BS < nb) {
             put(pr, st ^ 1);
             __syncthreads();
         }
     };
-    for (int c0 = 0; c0 < nb; c0 += 2 * MQ_BS) {
+    for (int c0 = 0; c0 < nb; c0 += 2 * BS) {
         round(c0, 0, L[0], L[1]);
-        if (c0 + MQ_BS < nb) round(c0 + MQ_BS, 1, L[1], L[0]);
+        if (c0 + BS < nb) round(c0 + BS, 1, L[1], L[0]);
     }
     // lane (q, n): row r0 + q of each set, token 16 * tile + n; groups 2i (even) and 2i + 1 (odd)
 #pragma unroll
@@ -1901,13 +1920,15 @@ static void launch_mm_q8(const MvArgs &a, int m, hipStream_t s) {
     // rows per block by the matrix height: enough waves for few rows, more
     // reuse of each staged activation for many
     const unsigned gy = (unsigned)((m + 63) / 64);
-    if (a.total_rows >= 16384) {
-        k_mm_q8<KIND, 2, 4><<<dim3((unsigned)((a.total_rows + 31) / 32), gy), 256, 0, s>>>(a, m);
-    } else if (a.total_rows >= 6144) {
-        k_mm_q8<KIND, 2, 2><<<dim3((unsigned)((a.total_rows + 15) / 16), gy), 256, 0, s>>>(a, m);
-    } else {
-        k_mm_q8<KIND, 2, 1><<<dim3((unsigned)((a.total_rows + 7) / 8), gy), 256, 0, s>>>(a, m);
-    }
+    // (sets, tiles, blocks per stage) measured at 64 tokens: 4096 rows
+    // (1, 2, 4) against (2, 1, 2) 46 / 59 us at 4096 columns, 126 / 164 us
+    // at 12288; 6144 rows (2, 2, 4) 63 against 72 us; 24576 rows (2, 4, 2)
+    // 137 against 142 us for 4 blocks per stage
+#define Q8L(S, T, B) k_mm_q8<KIND, S, T, B><<<dim3((unsigned)((a.total_rows + 4 * S * T - 1) / (4 * S * T)), gy), 256, 0, s>>>(a, m)
+    if (a.total_rows >= 16384) Q8L(2, 4, 2);
+    else if (a.total_rows >= 6144) Q8L(2, 2, 4);
+    else Q8L(1, 2, 4);
+#undef Q8L
 }
 
 // F16 / BF16 / F32 rows (4-byte aligned rows): stage = 64 elements x 64
