@@ -101,8 +101,17 @@ __device__ __forceinline__ void quant256(const float v[4], int lane, size_t blk,
         float d = amax / 127.0f;
         float id = d != 0.0f ? 1.0f / d : 0.0f;
         uint32_t packed = 0;
-        for (int k = 0; k < 4; k++) packed |= (uint32_t)(clampi(round_i(v[k] * id), -127, 127) & 0xFF) << (8 * k);
+        int qv[4];
+        for (int k = 0; k < 4; k++) {
+            qv[k] = clampi(round_i(v[k] * id), -127, 127);
+            packed |= (uint32_t)(qv[k] & 0xFF) << (8 * k);
+        }
         ((uint32_t *)(q80.qs + blk * 256))[lane] = packed;
+        if (q80.xh) {  // batches: the quants as f16 for the matrix-core products
+            const uint32_t h01 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)qv[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)qv[1]) << 16);
+            const uint32_t h23 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)qv[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)qv[3]) << 16);
+            ((uint2 *)(q80.xh + blk * 256))[lane] = make_uint2(h01, h23);
+        }
         if ((lane & 7) == 0) q80.d[blk * 8 + lane / 8] = d;
     }
 }

@@ -70,7 +70,7 @@ struct ActQ8K {
 struct ActQ8_0 {
     int8_t *qs;     // [rows][n]
     float *d;       // [rows][n/32]
-    uint16_t *xh;   // [rows][n] the quants as f16 (filled for batched products)
+    uint16_t *xh;   // [rows][n] the quants as f16, written for batches of 2 or more (matrix-core products)
 };
 
 // Bytes of an activation buffer for `rows` vectors of n elements.

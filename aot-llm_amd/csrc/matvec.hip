@@ -42,7 +42,7 @@ struct MvArgs {
     const int16_t *xbs;
     const float *xf;
     const int8_t *xt;  // Q8_K batches: the tiled copy of the quants (ActQ8K::qt)
-    uint16_t *xh;  // Q8_0 family, batches: the quants as f16 (written before the matmul)
+    uint16_t *xh;  // Q8_0 family, batches: the quants as f16 (written by the batch's quantizer)
     // K-quant rows, one token: when set, every block quantizes this f32
     // input to Q8_K itself (instead of reading xq / xd / xbs)
     const float *xq_src;
@@ -1685,8 +1685,9 @@ __device__ __forceinline__ float hsum8(const float (&c)[8]) {
 // acc_l = fma(f16(d) * y.d, P_l, acc_l) over blocks in order and the avx2
 // horizontal sum run on the VALU exactly as in the matvec.
 // Wave = SETS sets of 4 rows x TILES tiles of 16 tokens; block = 4 waves
-// over BR rows x 64 tokens. The activations arrive as f16 (k_q8_to_f16,
-// once per batch), the weights are converted to f16 when staged; both are
+// over BR rows x 64 tokens. The activations arrive as f16 (ActQ8_0::xh,
+// written by the batch's quantizer), the weights are converted to f16 when
+// staged; both are
 // staged in LDS, BS blocks per stage (2 or 4 by the matrix height), two
 // stages in LDS and two more in registers in flight.
 constexpr int MQ_BS = 2;   // blocks of 32 per stage
@@ -1705,18 +1706,6 @@ __device__ __forceinline__ void u8x4_to_f16(uint32_t u, float bias, uint32_t &lo
     const h2_t off = {(_Float16)(-1024.0f - bias), (_Float16)(-1024.0f - bias)};
     lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, l) + off);
     hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, h) + off);
-}
-
-// The batch's int8 quants as f16 (16 per thread).
-__global__ __launch_bounds__(256) void k_q8_to_f16(const int8_t *__restrict__ xq, uint16_t *__restrict__ xh, size_t n16) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n16) return;
-    const u32x4_t v = ((const u32x4_t *)xq)[i];
-    uint32_t h[8];
-#pragma unroll
-    for (int k = 0; k < 4; k++) u8x4_to_f16(v[k] ^ 0x80808080u, 128.0f, h[2 * k], h[2 * k + 1]);
-    ((u32x4_t *)xh)[2 * i] = u32x4_t{h[0], h[1], h[2], h[3]};
-    ((u32x4_t *)xh)[2 * i + 1] = u32x4_t{h[4], h[5], h[6], h[7]};
 }
 
 template <int KIND, int SETS, int TILES, int BS = MQ_BS>
@@ -1914,9 +1903,7 @@ __global__ __launch_bounds__(256) void k_mm_q8(MvArgs a, int m) {
 
 template <int KIND>
 static void launch_mm_q8(const MvArgs &a, int m, hipStream_t s) {
-    // the quants as f16 once per batch
-    const size_t n16 = (size_t)m * a.cols / 16;
-    k_q8_to_f16<<<(unsigned)((n16 + 255) / 256), 256, 0, s>>>(a.xq, a.xh, n16);
+    // (the quants as f16 come with the batch: written by its quantizer)
     // rows per block by the matrix height: enough waves for few rows, more
     // reuse of each staged activation for many
     const unsigned gy = (unsigned)((m + 63) / 64);

@@ -250,7 +250,7 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant4(const float *__restric
 }
 
 void launch_rmsnorm_quant(const float *x, const float *w, size_t n, size_t m, float eps, RmsOut out, hipStream_t s) {
-    if (m < 2) out.q8k.qt = nullptr;  // the tiled copy serves batches only
+    if (m < 2) out.q8k.qt = nullptr, out.q80.xh = nullptr;  // the tiled / f16 copies serve batches only
     if (n % 256 == 0 && n <= 4096) k_rmsnorm_quant4<1><<<(unsigned)m, SEQ_T, 0, s>>>(x, w, (int)n, eps, out);
     else if (n % 256 == 0) k_rmsnorm_quant4<2><<<(unsigned)m, SEQ_T, 0, s>>>(x, w, (int)n, eps, out);
     else k_rmsnorm_quant<<<(unsigned)m, SEQ_T, 0, s>>>(x, w, (int)n, eps, out);
@@ -269,7 +269,7 @@ __global__ void k_quant_f32(const float *__restrict__ x, int n, size_t total_blk
 }
 
 void launch_quant_f32(const float *x, size_t n, size_t m, RmsOut out, hipStream_t s) {
-    if (m < 2) out.q8k.qt = nullptr;  // the tiled copy serves batches only
+    if (m < 2) out.q8k.qt = nullptr, out.q80.xh = nullptr;  // the tiled / f16 copies serve batches only
     size_t total = m * n / 256;
     k_quant_f32<<<(unsigned)((total + 3) / 4), 256, 0, s>>>(x, (int)n, total, out);
 }
@@ -293,7 +293,7 @@ __global__ void k_glu_quant(const float *__restrict__ gate, const float *__restr
 }
 
 void launch_glu_quant(const float *gate, const float *up, size_t n, size_t m, int gelu, RmsOut out, hipStream_t s) {
-    if (m < 2) out.q8k.qt = nullptr;  // the tiled copy serves batches only
+    if (m < 2) out.q8k.qt = nullptr, out.q80.xh = nullptr;  // the tiled / f16 copies serve batches only
     size_t total = m * n / 256;
     k_glu_quant<<<(unsigned)((total + 3) / 4), 256, 0, s>>>(gate, up, (int)n, total, gelu, out);
 }
@@ -1449,7 +1449,7 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_add_quant4(float *x, const fl
 
 void launch_rmsnorm_add_quant(float *x, const float *y, const float *w_post, const float *w_next, size_t n, size_t m,
                               float eps, RmsOut out, hipStream_t s) {
-    if (m < 2) out.q8k.qt = nullptr;  // the tiled copy serves batches only
+    if (m < 2) out.q8k.qt = nullptr, out.q80.xh = nullptr;  // the tiled / f16 copies serve batches only
     if (n % 256 == 0 && n <= 4096) k_rmsnorm_add_quant4<1><<<(unsigned)m, SEQ_T, 0, s>>>(x, y, w_post, w_next, (int)n, eps, out);
     else if (n % 256 == 0) k_rmsnorm_add_quant4<2><<<(unsigned)m, SEQ_T, 0, s>>>(x, y, w_post, w_next, (int)n, eps, out);
     else k_rmsnorm_add_quant<<<(unsigned)m, SEQ_T, 0, s>>>(x, y, w_post, w_next, (int)n, eps, out);

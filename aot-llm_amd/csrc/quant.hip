@@ -400,7 +400,9 @@ __global__ void k_quant_q8_0(const float *__restrict__ x, size_t nblk, ActQ8_0 o
     for (int m = 1; m < 32; m <<= 1) amax = fmaxf(amax, shfl_xor(amax, m));
     float d = amax / 127.0f;
     float id = d != 0.0f ? 1.0f / d : 0.0f;
-    out.qs[i] = (int8_t)clampi(round_i(v * id), -127, 127);
+    const int q = clampi(round_i(v * id), -127, 127);
+    out.qs[i] = (int8_t)q;
+    if (out.xh) out.xh[i] = __builtin_bit_cast(uint16_t, (_Float16)q);
     if ((i & 31) == 0) out.d[blk] = d;
 }
 
@@ -413,6 +415,7 @@ void launch_quant_q8k(const float *x, size_t n, size_t rows, ActQ8K out, hipStre
 
 void launch_quant_q8_0(const float *x, size_t n, size_t rows, ActQ8_0 out, hipStream_t s) {
     size_t total = rows * n;
+    if (rows < 2) out.xh = nullptr;
     k_quant_q8_0<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(x, total / 32, out);
 }
 
@@ -450,6 +453,7 @@ __global__ void k_ref_to_q8_0(const aotk_block_q8_0 *in, size_t nblk, ActQ8_0 a)
     size_t b = i / 32;
     int e = (int)(i % 32);
     a.qs[i] = in[b].qs[e];
+    if (a.xh) a.xh[i] = __builtin_bit_cast(uint16_t, (_Float16)in[b].qs[e]);
     if (e == 0) a.d[b] = in[b].d;
 }
 
