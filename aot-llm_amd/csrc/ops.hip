@@ -982,12 +982,12 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
 //   ATT_ROWS_MAX: max, glibc-matched exp into LDS, the sequential sum by
 //   lane 0, then p = e * (1 / sum) written back over the scores; longer
 //   spans: k_attn_softmax_rows_x, a block per (row, head).
-//   k_attn_out_rows: one wave per (head, 64-dim slice, ATT_RB rows); lane d
-//   keeps the ATT_RB sums of dim d and adds p_t * v_t,d in position order;
+//   k_attn_out_rows: one wave per (head, 64-dim slice, ATT_RB rows: 2 at
+//   head_dim <= 128, 1 at 256); lane d keeps the ATT_RB sums of dim d and
+//   adds p_t * v_t,d in position order;
 //   V rows are read straight from the cache (256 B per wave per position),
 //   the probabilities with wave-uniform loads.
 constexpr int ATT_ROWS_MAX = 2048;  // spans of the one-wave softmax (four waves per block)
-constexpr int ATT_RB = 4;
 
 template <int NW, int CAP>
 __global__ __launch_bounds__(64 * NW) void k_attn_softmax_rows(AttnArgs a, int m) {
@@ -1017,9 +1017,9 @@ __global__ __launch_bounds__(64 * NW) void k_attn_softmax_rows(AttnArgs a, int m
     for (int t = lane; t < cnt; t += 64) ps[t] = ew[t] * inv;
 }
 
-template <int HD>
+template <int HD, int ATT_RB>
 __global__ __launch_bounds__(256) void k_attn_out_rows(AttnArgs a, int m) {
-    static_assert(ATT_RB == 4, "one float4 of p per position");
+    static_assert(ATT_RB == 4 || ATT_RB == 2 || ATT_RB == 1, "one float4 / float2 / float of p per position");
     __shared__ float4 sPr[4][32];
     constexpr int NS = HD / 64;
     const int lane = threadIdx.x & 63;
@@ -1073,15 +1073,29 @@ __global__ __launch_bounds__(256) void k_attn_out_rows(AttnArgs a, int m) {
             for (int r = 0; r < ATT_RB; r++) pv[r] = pr[r][c + (lane & 31)];
         };
         auto use = [&](const float (&v)[32], const float (&pv)[ATT_RB]) {
-            if (lane < 32) sp[lane] = make_float4(pv[0], pv[1], pv[2], pv[3]);
+            if (ATT_RB == 4) {
+                if (lane < 32) sp[lane] = make_float4(pv[0], pv[ATT_RB > 1 ? 1 : 0], pv[ATT_RB > 2 ? 2 : 0], pv[ATT_RB > 3 ? 3 : 0]);
+            } else if (ATT_RB == 2) {
+                if (lane < 32) ((float2 *)sp)[lane] = make_float2(pv[0], pv[ATT_RB > 1 ? 1 : 0]);
+            } else {
+                if (lane < 32) ((float *)sp)[lane] = pv[0];
+            }
             wave_lds_sync();
 #pragma unroll
             for (int k = 0; k < 32; k++) {
-                const float4 p4 = sp[k];
-                o[0] += p4.x * v[k];
-                o[1] += p4.y * v[k];
-                o[2] += p4.z * v[k];
-                o[3] += p4.w * v[k];
+                if (ATT_RB == 4) {
+                    const float4 p4 = sp[k];
+                    o[0] += p4.x * v[k];
+                    o[ATT_RB > 1 ? 1 : 0] += p4.y * v[k];
+                    o[ATT_RB > 2 ? 2 : 0] += p4.z * v[k];
+                    o[ATT_RB > 3 ? 3 : 0] += p4.w * v[k];
+                } else if (ATT_RB == 2) {
+                    const float2 p2 = ((const float2 *)sp)[k];
+                    o[0] += p2.x * v[k];
+                    o[ATT_RB > 1 ? 1 : 0] += p2.y * v[k];
+                } else {
+                    o[0] += ((const float *)sp)[k] * v[k];
+                }
             }
             wave_lds_sync();
         };
@@ -1164,12 +1178,16 @@ static void launch_rows(const AttnArgs &a, size_t head_dim, size_t m, size_t lon
     if (longest <= (size_t)ATT_ROWS_MAX) k_attn_softmax_rows<4, ATT_ROWS_MAX><<<(pairs + 3) / 4, 256, 0, s>>>(a, (int)m);
     else if (longest <= 8192) k_attn_softmax_rows_x<8192><<<pairs, SEQ_T, 0, s>>>(a, (int)m);
     else k_attn_softmax_rows_x<ATT_MAX_SPAN><<<pairs, SEQ_T, 0, s>>>(a, (int)m);
-    const size_t tasks = (m + ATT_RB - 1) / ATT_RB * a.n_head * (head_dim / 64);
+    // rows per wave (measured at 64 rows against 4: head_dim 128 two rows,
+    // 4096 positions 160 -> 127 us, 512 positions 25 -> 21 us; head_dim 256
+    // one row, 8192 positions 297 -> 213 us, a 1024 window 47 -> 30 us)
+    const int RB = head_dim == 256 ? 1 : 2;
+    const size_t tasks = (m + RB - 1) / RB * a.n_head * (head_dim / 64);
     const unsigned g = (unsigned)((tasks + 3) / 4);
     switch (head_dim) {
-    case 64: k_attn_out_rows<64><<<g, 256, 0, s>>>(a, (int)m); break;
-    case 128: k_attn_out_rows<128><<<g, 256, 0, s>>>(a, (int)m); break;
-    default: k_attn_out_rows<256><<<g, 256, 0, s>>>(a, (int)m); break;
+    case 64: k_attn_out_rows<64, 2><<<g, 256, 0, s>>>(a, (int)m); break;
+    case 128: k_attn_out_rows<128, 2><<<g, 256, 0, s>>>(a, (int)m); break;
+    default: k_attn_out_rows<256, 1><<<g, 256, 0, s>>>(a, (int)m); break;
     }
 }
 
