@@ -560,15 +560,18 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
     }
 }
 
-// LDS of one K-quant block: the activation records and the fold buffer.
+// LDS of one K-quant block: the activation records (one per super-block of
+// the row; sized to NB when it is known, so that short rows leave room for
+// more resident blocks) and the fold buffer.
+template <int NB>
 struct KqShared {
-    __align__(16) uint8_t y[64 * KQ_REC];
+    __align__(16) uint8_t y[(NB > 0 ? NB : 64) * KQ_REC];
     __align__(16) float t[4][256 + 16];  // [wave][row slot * ts + super-block] (+ read slack)
 };
 
 template <int KIND, int PF, int NB, bool QSRC = false>
 __global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq(MvArgs a, int RL, int G) {
-    __shared__ KqShared sh;
+    __shared__ KqShared<NB> sh;
     mv_kq_body<KIND, PF, NB, QSRC>(a, RL, G, blockIdx.x, sh.y, sh.t);
 }
 
@@ -578,7 +581,7 @@ __global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq(MvArgs a, int RL, int
 // PF as for mv_kq_body (launched with PF == 0).
 template <int KA, int KB, int NB, int PF>
 __global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq2(MvArgs a, int RLa, int Ga, MvArgs b, int RLb, int Gb, int nblk_a) {
-    __shared__ KqShared sh;
+    __shared__ KqShared<NB> sh;
     if ((int)blockIdx.x < nblk_a) mv_kq_body<KA, PF, NB>(a, RLa, Ga, blockIdx.x, sh.y, sh.t);
     else mv_kq_body<KB, PF, NB>(b, RLb, Gb, blockIdx.x - nblk_a, sh.y, sh.t);
 }
@@ -592,7 +595,7 @@ __global__ __launch_bounds__(256, PF ? 2 : 4) void k_mv_kq2(MvArgs a, int RLa, i
 template <int KIND, int NB>
 __global__ __launch_bounds__(256) void k_mv_kqw(MvArgs a) {
     static_assert(NB > 32 && NB <= 64, "rows of 33..64 super-blocks");
-    __shared__ __align__(16) uint8_t sY[64 * KQ_REC];
+    __shared__ __align__(16) uint8_t sY[NB * KQ_REC];
     __shared__ __align__(16) float sT[2][64];
     using Geo = KqGeom<KIND>;
     constexpr int CH = kq_chl<KIND, 2>();
@@ -1120,6 +1123,83 @@ __device__ __forceinline__ void mmx_tiles2(const MmB<KIND> &b, const uint4 (&at)
     }
 }
 
+// Q4_K on the K = 64 matrix cores with the sub-block scales folded into
+// the B operand. Every 6-bit scale is split into two 3-bit parts s_p (the
+// quants are <= 15, so q * s_p <= 105): each part's pre-scaled quants are
+// exact signed bytes, and v_mfma_i32_16x16x64_i8 of them against the
+// activations sums a super-block in four steps. The scaled integer sum of
+// the super-block is then C_0 + 8 * C_1, exactly the sum of
+// sc_j * (dot of sub-block j) that the matvec forms. The mins term keeps
+// its own product against the mins broadcast per sub-block. Lane l's 16
+// bytes of step pair J (values 64J + 8q .. +8 and 64J + 32 + 8q .. +8,
+// q = l / 16) are the A operand as the tiled copy holds it; B holds the
+// same values of the lane's row. (Q5_K the same way needs three 2-bit
+// parts and measured 4% slower than the per-sub-block products.)
+struct MmP {
+    mm_v4i bp[2][4];  // [scale part][step pair J]
+    uint32_t mn[8];   // the mins of the sub-blocks, each broadcast to 4 bytes
+    float dd, dm;
+};
+
+typedef unsigned short mm_u16x2 __attribute__((ext_vector_type(2)));
+// Byte-wise product of four bytes by s (every product below 128, so no
+// byte carries into the next): two 16-bit lanes of one packed multiply.
+__device__ __forceinline__ int mm_bmul(uint32_t w, uint32_t s) {
+    const mm_u16x2 a = __builtin_bit_cast(mm_u16x2, w), b = {(unsigned short)s, (unsigned short)s};
+    return (int)__builtin_bit_cast(uint32_t, a * b);
+}
+
+__device__ __forceinline__ void mm_prep64(const MmW<AOTK_Q4_K> &cur, MmP &b) {
+    int sc[8], mn[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) scale_min_k4(j, cur.hdr.y, cur.hdr.z, cur.hdr.w, sc[j], mn[j]);
+#pragma unroll
+    for (int J = 0; J < 4; J++) {
+        const uint2 qb = cur.q[J];
+        const uint32_t w[4] = {qb.x & 0x0F0F0F0Fu, qb.y & 0x0F0F0F0Fu, (qb.x >> 4) & 0x0F0F0F0Fu, (qb.y >> 4) & 0x0F0F0F0Fu};
+#pragma unroll
+        for (int pt = 0; pt < 2; pt++) {
+            const uint32_t sa = ((uint32_t)sc[2 * J] >> (3 * pt)) & 7u, sb = ((uint32_t)sc[2 * J + 1] >> (3 * pt)) & 7u;
+            b.bp[pt][J] = mm_v4i{mm_bmul(w[0], sa), mm_bmul(w[1], sa), mm_bmul(w[2], sb), mm_bmul(w[3], sb)};
+        }
+        b.mn[2 * J] = (uint32_t)mn[2 * J] * 0x01010101u;
+        b.mn[2 * J + 1] = (uint32_t)mn[2 * J + 1] * 0x01010101u;
+    }
+    b.dd = f16_to_f32(cur.hdr.x & 0xFFFFu);
+    b.dm = f16_to_f32(cur.hdr.x >> 16);
+}
+
+// Terms of two token tiles from pre-scaled operands (see MmP), the same f32
+// term per (row, token) as mm_tile.
+__device__ __forceinline__ void mmx_tiles2_64(const MmP &b, const uint4 (&at)[2][4], const float *sD, int sb, int t0, int q,
+                                              int lane, float (*slot)[64][4]) {
+    mm_v4i c[2][2], cm[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) cm[u] = c[u][0] = c[u][1] = mm_v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int J = 0; J < 4; J++)
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const mm_v4i a = __builtin_bit_cast(mm_v4i, at[u][J]);
+            const mm_v4i bm = {(int)b.mn[2 * J], (int)b.mn[2 * J], (int)b.mn[2 * J + 1], (int)b.mn[2 * J + 1]};
+            c[u][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b.bp[0][J], c[u][0], 0, 0, 0);
+            c[u][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b.bp[1][J], c[u][1], 0, 0, 0);
+            cm[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bm, cm[u], 0, 0, 0);
+        }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const float4 y4 = *(const float4 *)&sD[sb * 64 + 16 * (t0 + u) + 4 * q];
+        const float yd[4] = {y4.x, y4.y, y4.z, y4.w};
+        float term[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int sumi = c[u][0][i] + (c[u][1][i] << 3);
+            term[i] = (b.dd * yd[i]) * (float)sumi - (b.dm * yd[i]) * (float)cm[u][i];
+        }
+        *(float4 *)slot[t0 + u][lane] = make_float4(term[0], term[1], term[2], term[3]);
+    }
+}
+
 template <int KIND, int W>
 __global__ __launch_bounds__(64 * W) void k_mm_kx(MvArgs a, int m) {
     __shared__ __align__(16) float sD[MMX_MAX_NB * 64];    // [super-block][token]
@@ -1163,14 +1243,24 @@ __global__ __launch_bounds__(64 * W) void k_mm_kx(MvArgs a, int m) {
                 // the next item's weights: the next round of this group, or the first of the next group
                 if (sb + W < nb) mm_load<KIND>(nxt, rowp, drow, sb + W, nb, q);
                 else if (gn < ngroups) mm_load<KIND>(nxt, rown, drown, wave, nb, q);
-                MmB<KIND> b;
-                mm_prep<KIND>(cur, b);
                 uint4 at[2][4];
                 mmx_load2(at, a.xt, sb, 0, ntiles, tile_stride, lane);
-                mmx_tiles2<KIND>(b, at, sD, sb, 0, q, lane, sT[par][wave]);
-                if (ntiles > 2) {
-                    mmx_load2(at, a.xt, sb, 2, ntiles, tile_stride, lane);
-                    mmx_tiles2<KIND>(b, at, sD, sb, 2, q, lane, sT[par][wave]);
+                if constexpr (KIND != AOTK_Q4_K) {
+                    MmB<KIND> b;
+                    mm_prep<KIND>(cur, b);
+                    mmx_tiles2<KIND>(b, at, sD, sb, 0, q, lane, sT[par][wave]);
+                    if (ntiles > 2) {
+                        mmx_load2(at, a.xt, sb, 2, ntiles, tile_stride, lane);
+                        mmx_tiles2<KIND>(b, at, sD, sb, 2, q, lane, sT[par][wave]);
+                    }
+                } else {
+                    MmP b;
+                    mm_prep64(cur, b);
+                    mmx_tiles2_64(b, at, sD, sb, 0, q, lane, sT[par][wave]);
+                    if (ntiles > 2) {
+                        mmx_load2(at, a.xt, sb, 2, ntiles, tile_stride, lane);
+                        mmx_tiles2_64(b, at, sD, sb, 2, q, lane, sT[par][wave]);
+                    }
                 }
                 cur = nxt;
             }
