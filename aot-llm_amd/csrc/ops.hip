@@ -274,28 +274,35 @@ void launch_quant_f32(const float *x, size_t n, size_t m, RmsOut out, hipStream_
     k_quant_f32<<<(unsigned)((total + 3) / 4), 256, 0, s>>>(x, (int)n, total, out);
 }
 
-// silu_mul / gelu_mul (ops.rs:115-134) then quantization; one wave per 256.
-__global__ void k_glu_quant(const float *__restrict__ gate, const float *__restrict__ up, int n, size_t total_blk, int gelu,
-                            RmsOut out) {
-    const int lane = threadIdx.x & 63;
-    size_t gb = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+// silu_mul / gelu_mul (ops.rs:115-134) then quantization: block = one
+// quantization block of 256 values, one value per thread (the libm-matched
+// exp / tanh run once per lane, not four times in a row), then wave 0
+// quantizes the block from LDS.
+__global__ __launch_bounds__(256) void k_glu_quant(const float *__restrict__ gate, const float *__restrict__ up, int n,
+                                                   size_t total_blk, int gelu, RmsOut out) {
+    __shared__ __align__(16) float sv[256];
+    const size_t gb = blockIdx.x;
     if (gb >= total_blk) return;
-    size_t per = (size_t)n / 256;
-    size_t m = gb / per, b = gb % per;
-    size_t off = m * n + b * 256 + lane * 4;
-    float4 g4 = *(const float4 *)(gate + off);
-    float4 u4 = *(const float4 *)(up + off);
-    float g[4] = {g4.x, g4.y, g4.z, g4.w}, u[4] = {u4.x, u4.y, u4.z, u4.w};
-    float v[4];
-    for (int k = 0; k < 4; k++) v[k] = gelu ? gelu_f(g[k]) * u[k] : silu_f(g[k], u[k]);
-    if (out.f32) *(float4 *)(out.f32 + off) = make_float4(v[0], v[1], v[2], v[3]);
-    quant256(v, lane, b, q8k_row(out.q8k, m, n), q80_row(out.q80, m, n));
+    const int t = threadIdx.x;
+    const size_t per = (size_t)n / 256;
+    const size_t m = gb / per, b = gb % per;
+    const size_t off = m * n + b * 256 + t;
+    const float g = gate[off], u = up[off];
+    const float v = gelu ? gelu_f(g) * u : silu_f(g, u);
+    sv[t] = v;
+    if (out.f32) out.f32[off] = v;
+    __syncthreads();
+    if (t < 64) {
+        const float4 v4 = ((const float4 *)sv)[t];
+        float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+        quant256(vv, t, b, q8k_row(out.q8k, m, n), q80_row(out.q80, m, n));
+    }
 }
 
 void launch_glu_quant(const float *gate, const float *up, size_t n, size_t m, int gelu, RmsOut out, hipStream_t s) {
     if (m < 2) out.q8k.qt = nullptr, out.q80.xh = nullptr;  // the tiled / f16 copies serve batches only
     size_t total = m * n / 256;
-    k_glu_quant<<<(unsigned)((total + 3) / 4), 256, 0, s>>>(gate, up, (int)n, total, gelu, out);
+    k_glu_quant<<<(unsigned)total, 256, 0, s>>>(gate, up, (int)n, total, gelu, out);
 }
 
 // Embedding rows (dequant_row of the token's row, emit.rs:469) [* sqrt(dim)].
