@@ -756,21 +756,22 @@ __global__ __launch_bounds__(HD == 256 ? 64 * (QKD_MAX_GQA_256 + 1) : 576) void 
         kpre[j] = idx < rows * R4 && start + r != pos ? *(const float4 *)(kb + (size_t)r * kv + 4 * c4)
                                                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
+    // the new position's k and v go to the cache only after the block's
+    // barriers (a block barrier waits for the block's outstanding stores)
+    const bool owner = hg == gqa && pos >= start && pos < start + ATT_CH;
+    float vnew[HD / 64];
+    if (owner)
+#pragma unroll
+        for (int j = 0; j < HD / 64; j++) {
+            const int e = lane + 64 * j;
+            vnew[j] = p.v[(size_t)kvh * HD + e];
+            if (p.bv) vnew[j] = vnew[j] + p.bv[(size_t)kvh * HD + e];
+        }
     if (hg < gqa) {
         head_post_wave<HD>(sq[hg], sk + hg * HD, hin, p.bq != nullptr, p.q_norm != nullptr, (int)p.rot_dim, p.neox, p.eps);
     } else {
         float *kn = sq[ATT_MAX_GQA];
         head_post_wave<HD>(kn, sk + gqa * HD, hin, p.bk != nullptr, p.k_norm != nullptr, (int)p.rot_dim, p.neox, p.eps);
-        if (pos >= start && pos < start + ATT_CH) {
-            float *kc = p.k_cache + pos * kv + (size_t)kvh * HD;
-            float *vc = p.v_cache + pos * kv + (size_t)kvh * HD;
-            for (int e = lane; e < HD; e += 64) {
-                kc[e] = kn[e];
-                float v = p.v[(size_t)kvh * HD + e];
-                if (p.bv) v = v + p.bv[(size_t)kvh * HD + e];
-                vc[e] = v;
-            }
-        }
     }
     QK_TS(1);
     __syncthreads();  // the epilogue used sk for the squares of the norms
@@ -805,6 +806,15 @@ __global__ __launch_bounds__(HD == 256 ? 64 * (QKD_MAX_GQA_256 + 1) : 576) void 
         __syncthreads();
     }
     QK_TS(2);
+    if (owner) {
+        float *kc = p.k_cache + pos * kv + (size_t)kvh * HD;
+        float *vc = p.v_cache + pos * kv + (size_t)kvh * HD;
+#pragma unroll
+        for (int j = 0; j < HD / 64; j++) {
+            kc[lane + 64 * j] = sq[ATT_MAX_GQA][lane + 64 * j];
+            vc[lane + 64 * j] = vnew[j];
+        }
+    }
     if (hg >= gqa || lane >= rows) return;
     const float *kr = sk + lane * KS;
     const float *qq = sq[hg];
@@ -1377,7 +1387,6 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_add_quant(float *x, const flo
         if (i < n) {
             const float v = xv[k] + yv[k] * r * wv[k];
             xv[k] = v;
-            xr[i] = v;
             row[i] = v;
             sq[seq_idx(i, C)] = v * v;
         }
@@ -1389,6 +1398,7 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_add_quant(float *x, const flo
     for (int k = 0; k < 8; k++) {
         const int i = threadIdx.x + k * SEQ_T;
         if (i < n) {
+            xr[i] = xv[k];  // stored after the sums (see k_rmsnorm_add_quant4)
             const float v = row[i] * r2 * wn[k];
             row[i] = v;
             if (out.f32) out.f32[m * n + i] = v;
@@ -1452,7 +1462,6 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_add_quant4(float *x, const fl
             v.z = xv[k].z + yv[k].z * r * wv[k].z;
             v.w = xv[k].w + yv[k].w * r * wv[k].w;
             xv[k] = v;
-            xr[i] = v;
             squares(v, i);
         }
     }
@@ -1461,6 +1470,14 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_add_quant4(float *x, const fl
     const float r2 = 1.0f / sqrtf(ss2 / (float)n + eps);
     const ActQ8K qk = q8k_row(out.q8k, m, n);
     const ActQ8_0 q0 = q80_row(out.q80, m, n);
+    // the new x is stored only now: a store in flight would hold up every
+    // barrier of the second sum (a block barrier waits for the block's
+    // outstanding memory operations)
+#pragma unroll
+    for (int k = 0; k < KF; k++) {
+        const int i = tid + k * SEQ_T;
+        if (i < n4) xr[i] = xv[k];
+    }
 #pragma unroll
     for (int k = 0; k < KF; k++) {
         const int i = tid + k * SEQ_T;
