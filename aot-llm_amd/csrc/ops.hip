@@ -714,8 +714,8 @@ __device__ __forceinline__ void head_post_wave(float *hv, float *tmp, const Head
 constexpr int QKD_MAX_GQA_256 = 4;
 template <int HD>
 __global__ __launch_bounds__(HD == 256 ? 64 * (QKD_MAX_GQA_256 + 1) : 576) void k_attn_qk_decode(AttnArgs a, QkvPost p) {
-    constexpr int KS = HD + 1;
-    __shared__ float sk[ATT_CH * KS];
+    constexpr int KS = HD + 4;  // 16-byte rows; lanes reading 16 bytes of 16 rows hit all banks
+    __shared__ __align__(16) float sk[ATT_CH * KS];
     __shared__ __align__(16) float sq[ATT_MAX_GQA + 1][HD];
     const int gqa = a.n_head / a.n_kv_head;
     const int lane = threadIdx.x & 63, hg = threadIdx.x >> 6;
@@ -781,11 +781,7 @@ __global__ __launch_bounds__(HD == 256 ? 64 * (QKD_MAX_GQA_256 + 1) : 576) void 
         const int idx = threadIdx.x + j * nthreads;
         if (idx < rows * R4) {
             const int r = idx / R4, c4 = idx % R4;
-            float *d = sk + r * KS + 4 * c4;
-            d[0] = kpre[j].x;
-            d[1] = kpre[j].y;
-            d[2] = kpre[j].z;
-            d[3] = kpre[j].w;
+            *(float4 *)(sk + r * KS + 4 * c4) = kpre[j];
         }
     }
     for (int idx = threadIdx.x + PK * nthreads; idx < rows * R4; idx += nthreads) {
@@ -793,11 +789,7 @@ __global__ __launch_bounds__(HD == 256 ? 64 * (QKD_MAX_GQA_256 + 1) : 576) void 
         float4 k4;
         if (start + r == pos) k4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         else k4 = *(const float4 *)(kb + (size_t)r * kv + 4 * c4);
-        float *d = sk + r * KS + 4 * c4;
-        d[0] = k4.x;
-        d[1] = k4.y;
-        d[2] = k4.z;
-        d[3] = k4.w;
+        *(float4 *)(sk + r * KS + 4 * c4) = k4;
     }
     __syncthreads();
     if (pos >= start && pos < start + ATT_CH) {  // the new row
@@ -816,11 +808,17 @@ __global__ __launch_bounds__(HD == 256 ? 64 * (QKD_MAX_GQA_256 + 1) : 576) void 
         }
     }
     if (hg >= gqa || lane >= rows) return;
-    const float *kr = sk + lane * KS;
-    const float *qq = sq[hg];
+    const float4 *kr = (const float4 *)(sk + lane * KS);
+    const float4 *qq = (const float4 *)sq[hg];
     float sc = 0.0f;
-#pragma unroll 16
-    for (int d = 0; d < HD; d++) sc += qq[d] * kr[d];
+#pragma unroll 8
+    for (int d4 = 0; d4 < HD / 4; d4++) {
+        const float4 k4 = kr[d4], q4 = qq[d4];
+        sc += q4.x * k4.x;
+        sc += q4.y * k4.y;
+        sc += q4.z * k4.z;
+        sc += q4.w * k4.w;
+    }
     a.prob[(size_t)(kvh * gqa + hg) * a.span + (start + lane - t0)] = sc * a.scale;
     QK_TS(3);
 }
