@@ -1377,6 +1377,9 @@ __global__ __launch_bounds__(256) void k_mv_q80(MvArgs a) {
 // 256 threads), written to LDS; phase B: lane (row r, chain l) runs
 // acc_l = fma(D, P_l, acc_l) over the step's blocks in order. The next
 // step's weights are loaded during phase B. Then the avx2 horizontal sum.
+// Phase B runs on 8 * Q8B_R lanes (16 of the 64 with two rows per wave);
+// the others idle there, which measured cheaper than the larger phase A
+// that more rows per wave need.
 constexpr int Q8B_R = 2;  // measured: 2 rows per wave beat 4 (Q8_0 14336x4096 14.5 against 17.7 us) and 1
 constexpr int Q8B_MAX_COLS = 16384;
 constexpr int Q8B_CS = 64 + 4;  // floats per (row, chain) line of the P buffer: chain-major, padded
