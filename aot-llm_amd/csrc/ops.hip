@@ -1187,10 +1187,65 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_softmax_rows_x(AttnArgs a, int m
     }
 }
 
+// The same on 256 threads per (row, head) (spans up to CAP <= 8192): the
+// prompt runs m x n_head of these at once, so the issue count of the exact
+// sum matters more than its latency.
+template <int CAP>
+__global__ __launch_bounds__(256) void k_attn_softmax_rows_q(AttnArgs a, int m) {
+    constexpr int T = 256;
+    __shared__ __align__(16) float e[CAP + T + 32];
+    __shared__ SeqScratch S;
+    __shared__ float red[T / 64];
+    __shared__ uint64_t stab[32];
+    constexpr int SPT = CAP / T;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int i = blockIdx.x / a.n_head, h = blockIdx.x % a.n_head;
+    size_t t0, n;
+    row_range(a, i, t0, n);
+    const int cnt = (int)(n - t0);
+    float *ps = a.prob + ((size_t)i * a.n_head + h) * a.span;
+    exp_table_to_lds(stab);
+    float sv[SPT];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < SPT; k++) {
+        const int t = tid + k * T;
+        sv[k] = t < cnt ? ps[t] : -INFINITY;
+        mx = fmaxf(mx, sv[k]);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = wave_max(lane < T / 64 ? red[lane] : -INFINITY);
+    const int C = seq_chunk_of(cnt, T);
+#pragma unroll
+    for (int k = 0; k < SPT; k++) {
+        const int t = tid + k * T;
+        if (t < cnt) {
+            sv[k] = aotk_expf_tab(sv[k] - mx, stab);
+            e[seq_idx(t, C)] = sv[k];
+        }
+    }
+    __syncthreads();
+    const float inv = 1.0f / exact_seq_sum256(e, cnt, S);
+#pragma unroll
+    for (int k = 0; k < SPT; k++) {
+        const int t = tid + k * T;
+        if (t < cnt) ps[t] = sv[k] * inv;
+    }
+}
+
 
 static void launch_rows(const AttnArgs &a, size_t head_dim, size_t m, size_t longest, hipStream_t s) {
     const unsigned pairs = (unsigned)(m * a.n_head);
-    if (longest <= (size_t)ATT_ROWS_MAX) k_attn_softmax_rows<4, ATT_ROWS_MAX><<<(pairs + 3) / 4, 256, 0, s>>>(a, (int)m);
+    // many (row, head) pairs: the 256-thread exact sum for spans past 1024
+    // (measured at 64 rows x 32 heads: 4096 positions 64 -> 51 us); few
+    // pairs (8 heads at 8192 positions: 27 against 34 us) keep the
+    // 1024-thread form
+    const bool many = pairs >= 1024;
+    if (many && longest > 1024 && longest <= 4096) k_attn_softmax_rows_q<4096><<<pairs, 256, 0, s>>>(a, (int)m);
+    else if (many && longest > 4096 && longest <= 8192) k_attn_softmax_rows_q<8192><<<pairs, 256, 0, s>>>(a, (int)m);
+    else if (longest <= (size_t)ATT_ROWS_MAX) k_attn_softmax_rows<4, ATT_ROWS_MAX><<<(pairs + 3) / 4, 256, 0, s>>>(a, (int)m);
     else if (longest <= 8192) k_attn_softmax_rows_x<8192><<<pairs, SEQ_T, 0, s>>>(a, (int)m);
     else k_attn_softmax_rows_x<ATT_MAX_SPAN><<<pairs, SEQ_T, 0, s>>>(a, (int)m);
     // rows per wave (measured at 64 rows against 4: head_dim 128 two rows,

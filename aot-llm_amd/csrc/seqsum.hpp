@@ -50,10 +50,11 @@ constexpr int SEQ_MAX_N = 16384;
 constexpr int SEQ_T = 1024;
 constexpr int SEQ_PAD_N = SEQ_MAX_N + SEQ_T + 32;
 __device__ __forceinline__ int seq_threads(int n) { return n <= 1024 ? 256 : SEQ_T; }
-__device__ __forceinline__ int seq_chunk(int n) {
-    const int c = (n + seq_threads(n) - 1) / seq_threads(n);
+__device__ __forceinline__ int seq_chunk_of(int n, int t) {  // chunk length for t threads
+    const int c = (n + t - 1) / t;
     return c <= 1 ? 1 : 1 << (32 - __builtin_clz(c - 1));
 }
+__device__ __forceinline__ int seq_chunk(int n) { return seq_chunk_of(n, seq_threads(n)); }
 __device__ __forceinline__ int seq_idx(int k, int C) {
     const int lc = __builtin_ctz(C);
     return (k >> lc) * (C + 1) + (k & (C - 1));
@@ -211,7 +212,7 @@ template <int MAXC, int T>
 __device__ __forceinline__ float exact_seq_sum_t(const float *pp, int n, SeqScratch &S) {
     constexpr int NW = T / 64;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int C = seq_chunk(n);
+    const int C = seq_chunk_of(n, T);
     const bool act = tid < T;  // wave-uniform; idle waves only meet the barriers
     const int c0 = act ? min(tid * C, n) : n;
     const int len = min(c0 + C, n) - c0;
@@ -330,6 +331,18 @@ __device__ __forceinline__ float exact_seq_sum_t(const float *pp, int n, SeqScra
     __syncthreads();
     SEQ_TS(5);
     return S.result;
+}
+
+// The same sum on a block of 256 threads (n <= 8192; the inputs in the
+// layout of seq_idx with C = seq_chunk_of(n, 256)): about twice the latency
+// of the 1024-thread form, half its instructions, for kernels that run many
+// independent sums at once.
+__device__ __forceinline__ float exact_seq_sum256(const float *pp, int n, SeqScratch &S) {
+    const int C = seq_chunk_of(n, 256);
+    if (C <= 4) return exact_seq_sum_t<4, 256>(pp, n, S);
+    if (C <= 8) return exact_seq_sum_t<8, 256>(pp, n, S);
+    if (C <= 16) return exact_seq_sum_t<16, 256>(pp, n, S);
+    return exact_seq_sum_t<32, 256>(pp, n, S);
 }
 
 __device__ __forceinline__ float exact_seq_sum(const float *pp, int n, SeqScratch &S) {
