@@ -468,8 +468,8 @@ __global__ __launch_bounds__(512) void k_attn_scores(AttnArgs a) {
 constexpr int ATT_SRB = 4;
 template <int HD>
 __global__ __launch_bounds__(512) void k_attn_scores_rb(AttnArgs a, int m) {
-    constexpr int KS = HD + 1;
-    __shared__ float sk[ATT_CH * KS];
+    constexpr int KS = HD + 4;  // 16-byte rows; lanes reading 16 bytes of 16 rows hit all banks
+    __shared__ __align__(16) float sk[ATT_CH * KS];
     __shared__ __align__(16) float sq[ATT_SRB][ATT_MAX_GQA][HD];
     const int gqa = a.n_head / a.n_kv_head;
     const int lane = threadIdx.x & 63, hg = threadIdx.x >> 6;
@@ -499,25 +499,26 @@ __global__ __launch_bounds__(512) void k_attn_scores_rb(AttnArgs a, int m) {
     constexpr int R4 = HD / 4;
     for (int idx = threadIdx.x; idx < rows * R4; idx += nthreads) {
         const int r = idx / R4, c4 = idx % R4;
-        const float4 k4 = *(const float4 *)(kb + (size_t)r * kv + 4 * c4);
-        float *d = sk + r * KS + 4 * c4;
-        d[0] = k4.x;
-        d[1] = k4.y;
-        d[2] = k4.z;
-        d[3] = k4.w;
+        *(float4 *)(sk + r * KS + 4 * c4) = *(const float4 *)(kb + (size_t)r * kv + 4 * c4);
     }
     __syncthreads();
     if (lane >= rows) return;
     const size_t t = start + lane;
-    const float *kr = sk + lane * KS;
+    const float4 *kr = (const float4 *)(sk + lane * KS);
     float sc[ATT_SRB];
 #pragma unroll
     for (int r = 0; r < ATT_SRB; r++) sc[r] = 0.0f;
-#pragma unroll 8
-    for (int d = 0; d < HD; d++) {
-        const float kd = kr[d];
+#pragma unroll 2
+    for (int d4 = 0; d4 < HD / 4; d4++) {
+        const float4 k4 = kr[d4];
 #pragma unroll
-        for (int r = 0; r < ATT_SRB; r++) sc[r] += sq[r][hg][d] * kd;
+        for (int r = 0; r < ATT_SRB; r++) {
+            const float4 q4 = ((const float4 *)sq[r][hg])[d4];
+            sc[r] += q4.x * k4.x;
+            sc[r] += q4.y * k4.y;
+            sc[r] += q4.z * k4.z;
+            sc[r] += q4.w * k4.w;
+        }
     }
 #pragma unroll
     for (int r = 0; r < ATT_SRB; r++)
