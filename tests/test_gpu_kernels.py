@@ -196,6 +196,46 @@ def test_matmul_many_rows(aotk, oracle, kind):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), m
 
 
+def random_kquant_rows(kind, rows, cols, rng):
+    """K-quant rows of uniformly random bytes (every quant and every 6-bit
+    scale and min value, 63 included) with d = dmin = 2^-6: the edge of the
+    prompt kernels' exact integer ranges (quant x scale part products,
+    int32 sums)."""
+    sb = cols // 256
+    size = {Q4_K: 144, Q5_K: 176, Q6_K: 210}[kind]
+    raw = rng.integers(0, 256, size=(rows, sb, size), dtype=np.uint8)
+    half = np.frombuffer(np.float16(2.0 ** -6).tobytes(), dtype=np.uint8)
+    if kind == Q6_K:
+        raw[:, :, 208:210] = half  # d after ql, qh and the 16 scales
+    else:
+        raw[:, :, 0:2] = half      # d
+        raw[:, :, 2:4] = half      # dmin
+    return raw.reshape(rows, sb * size)
+
+
+@pytest.mark.parametrize("kind", [Q4_K, Q5_K, Q6_K], ids=lambda k: NAMES[k])
+def test_matmul_kquant_extreme_values(aotk, oracle, kind):
+    """Random-byte K-quant weights against activations that quantize to
+    +-127 in most places, through the whole-batch prompt kernel (2048+
+    rows: the scale-folded matrix-core path for Q4_K) and the split one
+    (fewer rows), bit-exact, at full and ragged batches."""
+    rng = np.random.default_rng(99 + kind)
+    cols = 1024
+    for rows in (2064, 300):
+        raw = random_kquant_rows(kind, rows, cols, rng)
+        w = aotk.Weight(kind, raw, rows, cols)
+        for m in (64, 40):
+            xs = [(np.sign(rng.standard_normal(cols)) * (1.0 + 0.01 * rng.random(cols))).astype(np.float32)
+                  for _ in range(m)]
+            acts = np.concatenate([oracle.quantize_act(kind, x) for x in xs])
+            got = aotk.matmul(w, acts, m)
+            ref = oracle.matmul(kind, raw, acts, m, rows, cols, pool=oracle.Pool(8)).reshape(m, rows)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (rows, m)
+            one = aotk.matvec(w, oracle.quantize_act(kind, xs[3]))
+            assert np.array_equal(one.view(np.uint32), ref[3].view(np.uint32)), (rows, "matvec")
+        w.free()
+
+
 @pytest.mark.parametrize("kind,rows,cols", [(Q4_K, 4096, 4096), (Q4_K, 1024, 4096), (Q6_K, 1024, 4096),
                                             (Q4_K, 14336, 4096), (Q6_K, 4096, 14336)],
                          ids=["wq", "wk", "wv", "gate", "down"])
