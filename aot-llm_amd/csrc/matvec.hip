@@ -1200,10 +1200,11 @@ __device__ __forceinline__ void mmx_tiles2_64(const MmP &b, const uint4 (&at)[2]
     }
 }
 
+// The 16-row groups g0, g0 + gs, ... (< the matrix's groups) of one matrix
+// for the block (see k_mm_kx); sD holds the batch's Q8_K d as
+// [super-block][token], staged by the caller.
 template <int KIND, int W>
-__global__ __launch_bounds__(64 * W) void k_mm_kx(MvArgs a, int m) {
-    __shared__ __align__(16) float sD[MMX_MAX_NB * 64];    // [super-block][token]
-    __shared__ __align__(16) float sT[2][W][4][64][4];     // [round parity][slot][tile][lane][i]
+__device__ __forceinline__ void mm_kx_body(const MvArgs &a, int m, int g0, int gs, const float *sD, float (*sT)[W][4][64][4]) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane >> 4, r16 = lane & 15;
@@ -1213,11 +1214,7 @@ __global__ __launch_bounds__(64 * W) void k_mm_kx(MvArgs a, int m) {
     const int ngroups = (a.total_rows + 15) / 16;
     const int rounds = (nb + W - 1) / W;
     const size_t tile_stride = (size_t)nb * 4096;
-    for (int idx = threadIdx.x; idx < mt * nb; idx += 64 * W) {
-        const int tk = idx / nb, sb = idx - tk * nb;
-        sD[sb * 64 + tk] = a.xd[idx];
-    }
-    // the wave's items: (row group g, super-block sb), groups strided by the grid
+    // the wave's items: (row group g, super-block sb)
     auto rows_of = [&](int g, const uint8_t *&rowp, const uint16_t *&drow) {
         const int grow = g * 16 + r16;
         int local;
@@ -1225,16 +1222,17 @@ __global__ __launch_bounds__(64 * W) void k_mm_kx(MvArgs a, int m) {
         rowp = seg_sel(sg, a.w[0], a.w[1], a.w[2]) + (size_t)local * nb * KqGeom<KIND>::RB;
         drow = KIND == AOTK_Q6_K ? (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb : nullptr;
     };
+    if (g0 >= ngroups) return;  // (block-uniform)
     const uint8_t *rowp, *rown;
     const uint16_t *drow, *drown;
-    int g = blockIdx.x;
+    int g = g0;
     rows_of(g, rowp, drow);
     MmW<KIND> cur, nxt;
     if (wave < nb) mm_load<KIND>(cur, rowp, drow, wave, nb, q);
-    __syncthreads();
+    __syncthreads();  // (the staged d: the first weights are in flight meanwhile)
     int par = 0;
-    for (; g < ngroups; g += gridDim.x) {
-        const int gn = g + gridDim.x;
+    for (; g < ngroups; g += gs) {
+        const int gn = g + gs;
         if (gn < ngroups) rows_of(gn, rown, drown);
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // waves < ntiles: tile `wave`
         for (int r = 0; r < rounds; r++, par ^= 1) {
@@ -1287,6 +1285,41 @@ __global__ __launch_bounds__(64 * W) void k_mm_kx(MvArgs a, int m) {
         rowp = rown;
         drow = drown;
     }
+    __syncthreads();  // the caller may reuse sT
+}
+
+// The batch's Q8_K d into LDS as [super-block][token].
+__device__ __forceinline__ void mm_kx_stage_d(const MvArgs &a, int m, float *sD, int nthreads) {
+    const int mt = min(64, m), nb = a.nb;
+    for (int idx = threadIdx.x; idx < mt * nb; idx += nthreads) {
+        const int tk = idx / nb, sb = idx - tk * nb;
+        sD[sb * 64 + tk] = a.xd[idx];
+    }
+}
+
+template <int KIND, int W>
+__global__ __launch_bounds__(64 * W) void k_mm_kx(MvArgs a, int m) {
+    __shared__ __align__(16) float sD[MMX_MAX_NB * 64];    // [super-block][token]
+    __shared__ __align__(16) float sT[2][W][4][64][4];     // [round parity][slot][tile][lane][i]
+    mm_kx_stage_d(a, m, sD, 64 * W);
+    mm_kx_body<KIND, W>(a, m, blockIdx.x, gridDim.x, sD, sT);
+}
+
+// Two matrices of different kinds on the same batch in one persistent
+// launch (the prompt's q/k and v): the grid walks the groups of `a`, then
+// those of `b`, as one list of items, so that the second matrix fills the
+// blocks the first leaves idle in its last round. Both share the staged d.
+template <int KA, int KB, int W>
+__global__ __launch_bounds__(64 * W) void k_mm_kx2(MvArgs a, MvArgs b, int m) {
+    __shared__ __align__(16) float sD[MMX_MAX_NB * 64];
+    __shared__ __align__(16) float sT[2][W][4][64][4];
+    mm_kx_stage_d(a, m, sD, 64 * W);
+    const int G = gridDim.x, ga = (a.total_rows + 15) / 16;
+    mm_kx_body<KA, W>(a, m, blockIdx.x, G, sD, sT);
+    // item i >= ga of the combined list is group i - ga of b; this block's
+    // first such item
+    const int first = (int)blockIdx.x + ((ga - (int)blockIdx.x + G - 1) / G) * G;  // smallest i >= ga, i = blockIdx.x (mod G)
+    mm_kx_body<KB, W>(b, m, first - ga, G, sD, sT);
 }
 
 // ------------------------------------------------------ Q8_0 / Q4_0 / Q5_0
@@ -2404,11 +2437,36 @@ bool matvec_pair_ok(const DevWeight &a, const DevWeight &b) {
     return ((a.kind == AOTK_Q4_K || a.kind == AOTK_Q5_K) && b.kind == AOTK_Q6_K) && a.cols == b.cols && a.nb <= 64;
 }
 
+template <int KA>
+static void launch_mm_kx2(const MvArgs &a, const MvArgs &b, int groups, int m, hipStream_t s) {
+    static int resident = 0;
+    if (!resident) {
+        int dev = 0, cus = 0, per = 0;
+        (void)hipGetDevice(&dev);
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k_mm_kx2<KA, AOTK_Q6_K, 8>, 512, 0);
+        resident = std::max(1, cus) * std::max(1, per);
+    }
+    k_mm_kx2<KA, AOTK_Q6_K, 8><<<dim3((unsigned)std::min(groups, resident)), 512, 0, s>>>(a, b, m);
+}
+
 void launch_matvec_pair(int na, const DevWeight *const wa[], float *const ya[], const DevWeight &wb, float *yb,
                         const void *x_act, size_t m, hipStream_t s) {
     if (m >= MM_MIN_TOKENS) {  // batches: the MFMA matmul per kind
-        launch_matvec_multi(na, wa, ya, x_act, m, s);
-        launch_matvec(wb, x_act, m, yb, nullptr, s);
+        MvArgs a = make_args(na, wa, ya, nullptr, x_act);
+        const DevWeight *wbs[1] = {&wb};
+        float *ybs[1] = {yb};
+        MvArgs b = make_args(1, wbs, ybs, nullptr, x_act);
+        if (m <= MM_TOK && a.xt && a.nb <= MMX_MAX_NB && a.total_rows >= 2048) {
+            // both on one persistent launch: b's groups fill the blocks a
+            // leaves idle in its last round
+            const int groups = (a.total_rows + 15) / 16 + (b.total_rows + 15) / 16;
+            if (wa[0]->kind == AOTK_Q4_K) launch_mm_kx2<AOTK_Q4_K>(a, b, groups, (int)m, s);
+            else launch_mm_kx2<AOTK_Q5_K>(a, b, groups, (int)m, s);
+            return;
+        }
+        launch_args(wa[0]->kind, a, m, s);
+        launch_args(wb.kind, b, m, s);
         return;
     }
     MvArgs a = make_args(na, wa, ya, nullptr, x_act);

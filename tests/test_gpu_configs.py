@@ -38,6 +38,24 @@ def test_config_prompt_and_greedy(aotk, oracle, name):
     gm.free()
 
 
+@pytest.mark.parametrize("name", ["llama3-8b-q4km", "gemma3-4b-q5km"])
+def test_config_full_prompt_chunk(aotk, oracle, name):
+    """A full 64-token prompt chunk and a ragged one (70 tokens in batches
+    of 64) at the real shapes: four token tiles through the prompt matmuls,
+    including the launch that runs q/k and v (different kinds) together."""
+    from aotk import configs
+    n_prompt = 70
+    spec, gm, st, ref = _pair(aotk, oracle, name, n_prompt + 1, 64)
+    toks = configs.prompt_tokens(2, n_prompt, spec.d["vocab"])
+    st.prompt(toks, batch=64)
+    ref.prompt(toks, batch=64)
+    a, b = st.logits(), ref.logits()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{name}: prompt logits differ"
+    ref.close()
+    st.free()
+    gm.free()
+
+
 @pytest.mark.parametrize("name,n_pos", [("qwen3-8b-q8_0", 4096), ("gemma3-4b-q5km", 8192)])
 def test_config_long_context_decode(aotk, oracle, name, n_pos):
     spec, gm, st, ref = _pair(aotk, oracle, name, n_pos + 2, 1)
