@@ -1033,9 +1033,10 @@ __global__ __launch_bounds__(64 * NW) void k_attn_softmax_rows(AttnArgs a, int m
     for (int t = lane; t < cnt; t += 64) ps[t] = ew[t] * inv;
 }
 
-template <int HD, int ATT_RB>
+template <int HD, int ATT_RB, int GS = 32>
 __global__ __launch_bounds__(256) void k_attn_out_rows(AttnArgs a, int m) {
     static_assert(ATT_RB == 4 || ATT_RB == 2 || ATT_RB == 1, "one float4 / float2 / float of p per position");
+    static_assert((GS == 32 || GS == 64) && GS * ATT_RB <= 128, "positions per group: the p slot holds 128 floats");
     __shared__ float4 sPr[4][32];
     constexpr int NS = HD / 64;
     const int lane = threadIdx.x & 63;
@@ -1080,25 +1081,25 @@ __global__ __launch_bounds__(256) void k_attn_out_rows(AttnArgs a, int m) {
         // slot as [position][row] so that one broadcast 16-byte read gives
         // the four rows' p of a position
         size_t t = alo;
-        float va[32], pa[ATT_RB], vbb[32], pb[ATT_RB];
+        float va[GS], pa[ATT_RB], vbb[GS], pb[ATT_RB];
         float4 *sp = sPr[wv];
-        auto load = [&](float (&v)[32], float (&pv)[ATT_RB], size_t c) {
+        auto load = [&](float (&v)[GS], float (&pv)[ATT_RB], size_t c) {
 #pragma unroll
-            for (int k = 0; k < 32; k++) v[k] = vb[(c + k) * kv];
+            for (int k = 0; k < GS; k++) v[k] = vb[(c + k) * kv];
 #pragma unroll
-            for (int r = 0; r < ATT_RB; r++) pv[r] = pr[r][c + (lane & 31)];
+            for (int r = 0; r < ATT_RB; r++) pv[r] = pr[r][c + (lane & (GS - 1))];
         };
-        auto use = [&](const float (&v)[32], const float (&pv)[ATT_RB]) {
+        auto use = [&](const float (&v)[GS], const float (&pv)[ATT_RB]) {
             if (ATT_RB == 4) {
-                if (lane < 32) sp[lane] = make_float4(pv[0], pv[ATT_RB > 1 ? 1 : 0], pv[ATT_RB > 2 ? 2 : 0], pv[ATT_RB > 3 ? 3 : 0]);
+                if (lane < GS) sp[lane] = make_float4(pv[0], pv[ATT_RB > 1 ? 1 : 0], pv[ATT_RB > 2 ? 2 : 0], pv[ATT_RB > 3 ? 3 : 0]);
             } else if (ATT_RB == 2) {
-                if (lane < 32) ((float2 *)sp)[lane] = make_float2(pv[0], pv[ATT_RB > 1 ? 1 : 0]);
+                if (lane < GS) ((float2 *)sp)[lane] = make_float2(pv[0], pv[ATT_RB > 1 ? 1 : 0]);
             } else {
-                if (lane < 32) ((float *)sp)[lane] = pv[0];
+                if (lane < GS) ((float *)sp)[lane] = pv[0];
             }
             wave_lds_sync();
 #pragma unroll
-            for (int k = 0; k < 32; k++) {
+            for (int k = 0; k < GS; k++) {
                 if (ATT_RB == 4) {
                     const float4 p4 = sp[k];
                     o[0] += p4.x * v[k];
@@ -1115,17 +1116,17 @@ __global__ __launch_bounds__(256) void k_attn_out_rows(AttnArgs a, int m) {
             }
             wave_lds_sync();
         };
-        if (t + 32 <= ahi) load(va, pa, t);
-        while (t + 32 <= ahi) {
-            const bool more = t + 64 <= ahi;
-            if (more) load(vbb, pb, t + 32);
+        if (t + GS <= ahi) load(va, pa, t);
+        while (t + GS <= ahi) {
+            const bool more = t + 2 * GS <= ahi;
+            if (more) load(vbb, pb, t + GS);
             use(va, pa);
-            t += 32;
+            t += GS;
             if (!more) break;
-            const bool more2 = t + 64 <= ahi;
-            if (more2) load(va, pa, t + 32);
+            const bool more2 = t + 2 * GS <= ahi;
+            if (more2) load(va, pa, t + GS);
             use(vbb, pb);
-            t += 32;
+            t += GS;
             if (!more2) break;
         }
         for (; t < ahi; t++) {
@@ -1253,12 +1254,22 @@ static void launch_rows(const AttnArgs &a, size_t head_dim, size_t m, size_t lon
     // 4096 positions 160 -> 127 us, 512 positions 25 -> 21 us; head_dim 256
     // one row, 8192 positions 297 -> 213 us, a 1024 window 47 -> 30 us)
     const int RB = head_dim == 256 ? 1 : 2;
+    // V loads 64 positions ahead instead of 32 for long spans (measured:
+    // Qwen3 4096 positions 126 -> 118 us, Gemma-3 8192 206 -> 194 us,
+    // a 1024 window 29 -> 28 us; 512 positions 21 -> 23 us)
+    const bool deep = longest >= 1024;
     const size_t tasks = (m + RB - 1) / RB * a.n_head * (head_dim / 64);
     const unsigned g = (unsigned)((tasks + 3) / 4);
     switch (head_dim) {
     case 64: k_attn_out_rows<64, 2><<<g, 256, 0, s>>>(a, (int)m); break;
-    case 128: k_attn_out_rows<128, 2><<<g, 256, 0, s>>>(a, (int)m); break;
-    default: k_attn_out_rows<256, 1><<<g, 256, 0, s>>>(a, (int)m); break;
+    case 128:
+        if (deep) k_attn_out_rows<128, 2, 64><<<g, 256, 0, s>>>(a, (int)m);
+        else k_attn_out_rows<128, 2><<<g, 256, 0, s>>>(a, (int)m);
+        break;
+    default:
+        if (deep) k_attn_out_rows<256, 1, 64><<<g, 256, 0, s>>>(a, (int)m);
+        else k_attn_out_rows<256, 1><<<g, 256, 0, s>>>(a, (int)m);
+        break;
     }
 }
 
