@@ -1008,8 +1008,11 @@ constexpr int ATT_ROWS_MAX = 2048;  // spans of the one-wave softmax (four waves
 template <int NW, int CAP>
 __global__ __launch_bounds__(64 * NW) void k_attn_softmax_rows(AttnArgs a, int m) {
     __shared__ __align__(16) float e[NW][CAP];
+    __shared__ uint64_t stab[32];  // expf's 2^(i/32) table (an LDS read per lookup)
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int pair = blockIdx.x * NW + w;
+    exp_table_to_lds(stab);
+    __syncthreads();
     if (pair >= m * a.n_head) return;
     const int i = pair / a.n_head, h = pair % a.n_head;
     size_t t0, n;
@@ -1017,20 +1020,37 @@ __global__ __launch_bounds__(64 * NW) void k_attn_softmax_rows(AttnArgs a, int m
     const int cnt = (int)(n - t0);
     float *ps = a.prob + ((size_t)i * a.n_head + h) * a.span;
     float *ew = e[w];
+    // every score load of the lane in flight together (a loop that stores
+    // each one as it arrives waits for the loads one at a time)
+    constexpr int VPL = CAP / 64;
+    float v[VPL];
     float mx = -INFINITY;
-    for (int t = lane; t < cnt; t += 64) {
-        const float v = ps[t];
-        ew[t] = v;
-        mx = fmaxf(mx, v);
+#pragma unroll
+    for (int k = 0; k < VPL; k++) {
+        const int t = lane + 64 * k;
+        v[k] = t < cnt ? ps[t] : -INFINITY;
     }
+#pragma unroll
+    for (int k = 0; k < VPL; k++) mx = fmaxf(mx, v[k]);
     mx = wave_max(mx);
-    for (int t = lane; t < cnt; t += 64) ew[t] = aotk_expf(ew[t] - mx);
+#pragma unroll
+    for (int k = 0; k < VPL; k++) {
+        const int t = lane + 64 * k;
+        if (t < cnt) {
+            v[k] = aotk_expf_tab(v[k] - mx, stab);
+            ew[t] = v[k];
+        }
+    }
     if (cnt + lane < ((cnt + 63) & ~63)) ew[cnt + lane] = -0.0f;  // neutral padding to a run of 64
     wave_lds_sync();
     float sum = 0.0f;
     if (lane == 0) sum = seq_sum_lds_pad64(ew, cnt);
     const float inv = 1.0f / readlane_f(sum, 0);
-    for (int t = lane; t < cnt; t += 64) ps[t] = ew[t] * inv;
+#pragma unroll
+    for (int k = 0; k < VPL; k++) {
+        const int t = lane + 64 * k;
+        if (t < cnt) ps[t] = v[k] * inv;
+    }
 }
 
 template <int HD, int ATT_RB, int GS = 32>
