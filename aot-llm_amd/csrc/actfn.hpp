@@ -79,6 +79,25 @@ __device__ __forceinline__ Q8KLane q8k_lane(const float v[4], int lane) {
     return r;
 }
 
+// One lane's share of the 8 Q8_0 blocks (quant.rs:231-245) of 256 values
+// held 4 per lane (element 4*lane + k; lanes 8j..8j+7 hold block j): the
+// packed quants, the quants themselves and the block scale d.
+__device__ __forceinline__ uint32_t q80_lane(const float v[4], int (&qv)[4], float &d) {
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = fmaxf(amax, dppx_f<DPP_XOR1>(amax));
+    amax = fmaxf(amax, dppx_f<DPP_XOR2>(amax));
+    amax = fmaxf(amax, dppx_f<DPP_HALF_MIRROR>(amax));
+    d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        qv[k] = clampi(round_i(v[k] * id), -127, 127);
+        packed |= (uint32_t)(qv[k] & 0xFF) << (8 * k);
+    }
+    return packed;
+}
+
 // Quantize 256 values held 4 per lane (element 4*lane + k) of one wave into
 // the Q8_K block `blk` (quant.rs:248-283) and/or the 8 Q8_0 blocks
 // 8*blk .. 8*blk+7 (quant.rs:231-245).
@@ -94,18 +113,9 @@ __device__ __forceinline__ void quant256(const float v[4], int lane, size_t blk,
         if (lane == 0) q8k.d[blk] = r.d;
     }
     if (q80.qs) {
-        float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        amax = fmaxf(amax, dppx_f<DPP_XOR1>(amax));
-        amax = fmaxf(amax, dppx_f<DPP_XOR2>(amax));
-        amax = fmaxf(amax, dppx_f<DPP_HALF_MIRROR>(amax));
-        float d = amax / 127.0f;
-        float id = d != 0.0f ? 1.0f / d : 0.0f;
-        uint32_t packed = 0;
         int qv[4];
-        for (int k = 0; k < 4; k++) {
-            qv[k] = clampi(round_i(v[k] * id), -127, 127);
-            packed |= (uint32_t)(qv[k] & 0xFF) << (8 * k);
-        }
+        float d;
+        const uint32_t packed = q80_lane(v, qv, d);
         ((uint32_t *)(q80.qs + blk * 256))[lane] = packed;
         if (q80.xh) {  // batches: the quants as f16 for the matrix-core products
             const uint32_t h01 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)qv[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)qv[1]) << 16);

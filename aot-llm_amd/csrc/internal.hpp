@@ -179,8 +179,9 @@ struct SampleArgs {
 };
 size_t sampler_scratch_bytes(size_t vocab);
 void launch_sample(const SampleArgs &p, hipStream_t s);
-// One token through a K-quant matrix of <= 64 super-blocks per row, the f32
-// input quantized to Q8_K inside the launch (same bytes as launch_quant_f32).
+// One token, the f32 input quantized inside the launch (same bytes as
+// launch_quant_f32): K-quant rows of <= 64 super-blocks (to Q8_K), Q8_0 /
+// Q4_0 / Q5_0 rows of cols % 256 == 0, cols <= 16384 (to Q8_0).
 // Returns false (nothing launched) for other kinds and widths.
 bool launch_matvec_quant(const DevWeight &w, const float *x, float *y, const float *add, hipStream_t s);
 void launch_matvec_multi(int n, const DevWeight *const ws[], float *const ys[], const void *x_act, size_t m,

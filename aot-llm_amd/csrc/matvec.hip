@@ -43,10 +43,19 @@ struct MvArgs {
     const float *xf;
     const int8_t *xt;  // Q8_K batches: the tiled copy of the quants (ActQ8K::qt)
     uint16_t *xh;  // Q8_0 family, batches: the quants as f16 (written by the batch's quantizer)
-    // K-quant rows, one token: when set, every block quantizes this f32
-    // input to Q8_K itself (instead of reading xq / xd / xbs)
+    // one token: when set, every block quantizes this f32 input itself
+    // (K-quant rows to Q8_K, Q8_0 / Q4_0 / Q5_0 rows to Q8_0) instead of
+    // reading xq / xd / xbs
     const float *xq_src;
 };
+
+// Ties v to this point of the program: loads before it stay before it and
+// uses of v stay after it (a volatile asm with a memory clobber).
+__device__ __forceinline__ void pin_after_loads(float4 &v) {
+    float x = v.x, y = v.y, z = v.z, w = v.w;
+    asm volatile("" : "+v"(x), "+v"(y), "+v"(z), "+v"(w) : : "memory");
+    v = make_float4(x, y, z, w);
+}
 
 // Segment of a global row (constant indices only, so that the kernel
 // arguments stay in scalar registers).
@@ -478,6 +487,12 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
         for (int k = 0; k < 4; k++) xf[k] = ((const float4 *)(a.xq_src + (size_t)min(wave + 4 * k, nb - 1) * 256))[lane];
     }
     load(cur, dcur, 0);
+    // the f32 input's loads stay ahead of the weights' and its quantization
+    // after them (no code motion across this point): the quantizer then
+    // waits for the input only, with the weights in flight
+    if constexpr (!stage)
+#pragma unroll
+        for (int k = 0; k < 4; k++) pin_after_loads(xf[k]);
     if constexpr (stage) {
         // unconditional stores: past the end they repeat the last element
 #pragma unroll
@@ -491,11 +506,19 @@ __device__ __forceinline__ void mv_kq_body(const MvArgs &a, int RL, int G, int b
     } else {
         // quantize the f32 input here, wave w taking super-blocks w, w + 4,
         // ... (the device quantizer of k_quant_f32, quant.rs:248-283)
+        // The first four super-blocks of the wave come from the loads issued
+        // before the weights' (xf); later ones are loaded here. (A select
+        // between xf and a load makes the load unconditional, after the
+        // weights', and the wait for it then waits for the weights too.)
         for (int b0 = wave; b0 < nb; b0 += 16) {
-            float4 v4[4];  // four super-blocks' loads in flight together (the first four loaded above)
+            float4 v4[4];  // four super-blocks' loads in flight together
+            if (b0 == wave) {
 #pragma unroll
-            for (int k = 0; k < 4; k++)
-                v4[k] = b0 == wave ? xf[k] : ((const float4 *)(a.xq_src + (size_t)min(b0 + 4 * k, nb - 1) * 256))[lane];
+                for (int k = 0; k < 4; k++) v4[k] = xf[k];
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; k++) v4[k] = ((const float4 *)(a.xq_src + (size_t)min(b0 + 4 * k, nb - 1) * 256))[lane];
+            }
             Q8KLane rq[4];  // independent: their reductions interleave
 #pragma unroll
             for (int k = 0; k < 4; k++) {
@@ -1424,7 +1447,7 @@ struct Q8bW {
     uint16_t d;
 };
 
-template <int KIND>
+template <int KIND, bool XQ = false>
 __global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
     constexpr int R = Q8B_R;
     // the activation (cols int8 quants, then cols / 32 scales), sized by the
@@ -1468,23 +1491,63 @@ __global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
     // scale per thread, indices past the end re-read the last), then the
     // first two steps' weights: the wait for the activation leaves those in
     // flight
-    const uint4 *xq = (const uint4 *)(a.xq + (size_t)tok * a.cols);
-    const int nq = (int)(a.cols / 16);
-    uint4 xv[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) xv[k] = xq[min(tid + 256 * k, nq - 1)];
-    float xdv[2];
-#pragma unroll
-    for (int k = 0; k < 2; k++) xdv[k] = a.xd[(size_t)tok * nb + min(tid + 256 * k, nb - 1)];
     Q8bW<KIND> cur[R], nxt[R];
-    load(cur, 0);
-    load(nxt, 64);
-    // (unconditional stores: past the end they repeat the last element's
-    // value at its own place, which keeps the loads above unconditional too)
+    if constexpr (!XQ) {
+        const uint4 *xq = (const uint4 *)(a.xq + (size_t)tok * a.cols);
+        const int nq = (int)(a.cols / 16);
+        uint4 xv[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++) ((uint4 *)sy)[min(tid + 256 * k, nq - 1)] = xv[k];
+        for (int k = 0; k < 4; k++) xv[k] = xq[min(tid + 256 * k, nq - 1)];
+        float xdv[2];
 #pragma unroll
-    for (int k = 0; k < 2; k++) syd[min(tid + 256 * k, nb - 1)] = xdv[k];
+        for (int k = 0; k < 2; k++) xdv[k] = a.xd[(size_t)tok * nb + min(tid + 256 * k, nb - 1)];
+        load(cur, 0);
+        load(nxt, 64);
+        // (unconditional stores: past the end they repeat the last element's
+        // value at its own place, which keeps the loads above unconditional too)
+#pragma unroll
+        for (int k = 0; k < 4; k++) ((uint4 *)sy)[min(tid + 256 * k, nq - 1)] = xv[k];
+#pragma unroll
+        for (int k = 0; k < 2; k++) syd[min(tid + 256 * k, nb - 1)] = xdv[k];
+    } else {
+        // one token, the f32 input (a.xq_src, cols % 256 == 0) quantized to
+        // Q8_0 here by every block (the quantizer of k_quant_f32): wave w
+        // takes the 256-value groups w, w + 4, ..., four loads in flight
+        const int ng = (int)(a.cols / 256);
+        float4 xf[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) xf[k] = ((const float4 *)(a.xq_src + (size_t)min(wave + 4 * k, ng - 1) * 256))[lane];
+        load(cur, 0);
+        load(nxt, 64);
+        // the input's loads stay ahead of the weights' and its quantization
+        // after them (no code motion across this point): the quantizer then
+        // waits for the input only, with the weights in flight
+#pragma unroll
+        for (int k = 0; k < 4; k++) pin_after_loads(xf[k]);
+        // (the first four groups straight from xf, not through a select
+        // with a load: that load would issue after the weights' and its wait
+        // would wait for them)
+        for (int g0 = wave; g0 < ng; g0 += 16) {
+            float4 v4[4];
+            if (g0 == wave) {
+#pragma unroll
+                for (int k = 0; k < 4; k++) v4[k] = xf[k];
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; k++) v4[k] = ((const float4 *)(a.xq_src + (size_t)min(g0 + 4 * k, ng - 1) * 256))[lane];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int g = g0 + 4 * k;
+                if (g >= ng) break;
+                const float v[4] = {v4[k].x, v4[k].y, v4[k].z, v4[k].w};
+                int qv[4];
+                float d;
+                ((uint32_t *)(sy + g * 256))[lane] = q80_lane(v, qv, d);
+                if ((lane & 7) == 0) syd[g * 8 + (lane >> 3)] = d;
+            }
+        }
+    }
     __syncthreads();
     const int rr = lane >> 3, chain = lane & 7;
     float acc = 0.0f;
@@ -2418,11 +2481,22 @@ void launch_matvec_multi(int n, const DevWeight *const ws[], float *const ys[], 
 
 bool launch_matvec_quant(const DevWeight &w, const float *x, float *y, const float *add, hipStream_t s) {
     const int kind = w.kind;
-    if ((kind != AOTK_Q4_K && kind != AOTK_Q5_K && kind != AOTK_Q6_K) || w.nb > 64)
-        return false;
     const DevWeight *ws[1] = {&w};
     float *ys[1] = {y};
     const float *adds[1] = {add};
+    if (kind == AOTK_Q8_0 || kind == AOTK_Q4_0 || kind == AOTK_Q5_0) {
+        if (w.cols % 256 != 0 || w.cols > (size_t)Q8B_MAX_COLS) return false;
+        ActQ8_0 none = {};
+        MvArgs a = make_args(1, ws, ys, adds, &none);
+        a.xq_src = x;
+        const dim3 grid((unsigned)((a.total_rows + 4 * Q8B_R - 1) / (4 * Q8B_R)), 1);
+        if (kind == AOTK_Q8_0) k_mv_q8b<AOTK_Q8_0, true><<<grid, 256, q8b_lds(a), s>>>(a);
+        else if (kind == AOTK_Q4_0) k_mv_q8b<AOTK_Q4_0, true><<<grid, 256, q8b_lds(a), s>>>(a);
+        else k_mv_q8b<AOTK_Q5_0, true><<<grid, 256, q8b_lds(a), s>>>(a);
+        return true;
+    }
+    if ((kind != AOTK_Q4_K && kind != AOTK_Q5_K && kind != AOTK_Q6_K) || w.nb > 64)
+        return false;
     ActQ8K none = {};
     MvArgs a = make_args(1, ws, ys, adds, &none);
     a.xq_src = x;

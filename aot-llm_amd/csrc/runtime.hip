@@ -382,6 +382,13 @@ int aotk_matmul_noalloc(const aotk_weight *w, const void *xs_dev, size_t m, floa
 int aotk_matvec_f32(const aotk_weight *w, const float *x_dev, float *out_dev) {
     if (!w) return fail("null weight");
     const DevWeight &dw = w->dw;
+    // where the kind and width allow, one launch: the matvec quantizes the
+    // input itself (the same quants as the separate quantizer below)
+    if (launch_matvec_quant(dw, x_dev, out_dev, nullptr, g_stream)) {
+        HIPC(hipGetLastError());
+        HIPC(hipStreamSynchronize(g_stream));
+        return 0;
+    }
     int a = activation(dw.kind);
     const void *act = x_dev;
     ActQ8K qk;
