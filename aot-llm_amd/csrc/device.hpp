@@ -16,7 +16,10 @@ namespace aotk {
 __device__ __forceinline__ float f16_to_f32(uint32_t h) {
     const float hw = (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
     const uint32_t special = ((h & 0x8000u) << 16) | 0x7F800000u | ((h & 0x3FFu) << 13);
-    return (h & 0x7C00u) == 0x7C00u ? __uint_as_float(special) : hw;
+    // all ones for exponent 31 (Inf / NaN), else zero: a mask, not a
+    // compare, so that no branch (and no early wait for a loaded h) forms
+    const uint32_t m = 0u - ((((h & 0x7C00u) + 0x400u) >> 15) & 1u);
+    return __uint_as_float((special & m) | (__float_as_uint(hw) & ~m));
 }
 
 // f32 -> binary16, round to nearest even (quant.rs:128-162).
