@@ -1312,11 +1312,22 @@ __device__ __forceinline__ void mm_kx_body(const MvArgs &a, int m, int g0, int g
 }
 
 // The batch's Q8_K d into LDS as [super-block][token].
-__device__ __forceinline__ void mm_kx_stage_d(const MvArgs &a, int m, float *sD, int nthreads) {
-    const int mt = min(64, m), nb = a.nb;
-    for (int idx = threadIdx.x; idx < mt * nb; idx += nthreads) {
-        const int tk = idx / nb, sb = idx - tk * nb;
-        sD[sb * 64 + tk] = a.xd[idx];
+template <int NT>
+__device__ __forceinline__ void mm_kx_stage_d(const MvArgs &a, int m, float *sD) {
+    // every load first (unconditional: indices past the end re-read the
+    // last), then the stores: one wait instead of one per element
+    constexpr int PER = (MMX_MAX_NB * 64 + NT - 1) / NT;
+    const int mt = min(64, m), nb = a.nb, tot = mt * nb;
+    float v[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) v[j] = a.xd[min((int)threadIdx.x + j * NT, tot - 1)];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int idx = threadIdx.x + j * NT;
+        if (idx < tot) {
+            const int tk = idx / nb, sb = idx - tk * nb;
+            sD[sb * 64 + tk] = v[j];
+        }
     }
 }
 
@@ -1324,7 +1335,7 @@ template <int KIND, int W>
 __global__ __launch_bounds__(64 * W) void k_mm_kx(MvArgs a, int m) {
     __shared__ __align__(16) float sD[MMX_MAX_NB * 64];    // [super-block][token]
     __shared__ __align__(16) float sT[2][W][4][64][4];     // [round parity][slot][tile][lane][i]
-    mm_kx_stage_d(a, m, sD, 64 * W);
+    mm_kx_stage_d<64 * W>(a, m, sD);
     mm_kx_body<KIND, W>(a, m, blockIdx.x, gridDim.x, sD, sT);
 }
 
@@ -1336,7 +1347,7 @@ template <int KA, int KB, int W>
 __global__ __launch_bounds__(64 * W) void k_mm_kx2(MvArgs a, MvArgs b, int m) {
     __shared__ __align__(16) float sD[MMX_MAX_NB * 64];
     __shared__ __align__(16) float sT[2][W][4][64][4];
-    mm_kx_stage_d(a, m, sD, 64 * W);
+    mm_kx_stage_d<64 * W>(a, m, sD);
     const int G = gridDim.x, ga = (a.total_rows + 15) / 16;
     mm_kx_body<KA, W>(a, m, blockIdx.x, G, sD, sT);
     // item i >= ga of the combined list is group i - ga of b; this block's
