@@ -12,5 +12,5 @@ from .abi import AotkError  # noqa: F401
 from .runtime import (  # noqa: F401
     DeviceBuffer, Model, Sampler, copy_dev, State, Weight, argmax, attention, dequant_rows, gelu_mul, init, matmul, matmul2, matmul_noalloc, matvec, matvec2, matvec3,
     matvec_f32, quantize_q8_0, quantize_q8_k, quantize_rows, rmsnorm, rmsnorm_heads, rope, silu_mul, softmax,
-    stream, sync, time_matvec, time_matmul,
+    stream, sync, time_hbm, time_matvec, time_matmul,
 )

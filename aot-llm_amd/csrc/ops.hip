@@ -1336,7 +1336,9 @@ void launch_attention(float *out, const float *q, const float *k_cache, const fl
     size_t span = window > 0 && window < ctx_rows ? window : ctx_rows;
     dim3 grid((unsigned)n_kv_head, (unsigned)((span + ATT_CH - 1) / ATT_CH), (unsigned)m);
     const unsigned threads = (unsigned)(64 * (n_head / n_kv_head));
-    if (m > 1 && !pos_dev && head_dim == 256 && n_head / n_kv_head <= 8) {
+    const size_t gqa_ratio = n_head / n_kv_head;
+    if (m > 1 && !pos_dev && head_dim == 256 &&
+        (gqa_ratio == 1 || gqa_ratio == 2 || gqa_ratio == 4 || gqa_ratio == 8)) {
         // head_dim 256: rows batched per block, q through the scalar unit
         // (measured at 64 rows: 8192 positions 839 -> 188 us, a 1024 window
         // 68 -> 43 us; at head_dim 128 the per-row-group kernel below stays
@@ -1348,7 +1350,7 @@ void launch_attention(float *out, const float *q, const float *k_cache, const fl
         case 1: k_attn_scores_sg<256, 1, 4><<<g4, 64, 0, s>>>(a, (int)m); break;
         case 2: k_attn_scores_sg<256, 2, 4><<<g4, 128, 0, s>>>(a, (int)m); break;
         case 4: k_attn_scores_sg<256, 4, 4><<<g4, 256, 0, s>>>(a, (int)m); break;
-        default: k_attn_scores_sg<256, 8, 4><<<g4, 512, 0, s>>>(a, (int)m); break;
+        case 8: k_attn_scores_sg<256, 8, 4><<<g4, 512, 0, s>>>(a, (int)m); break;
         }
     } else if (m > 1 && !pos_dev && head_dim <= 128) {
         // several rows per block over absolute position chunks

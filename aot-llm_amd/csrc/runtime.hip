@@ -93,6 +93,7 @@ int aotk_init(int device) {
     int n = 0;
     HIPC(hipGetDeviceCount(&n));
     if (device < 0 || device >= n) return fail("aotk_init: device %d out of range (%d devices)", device, n);
+    if (device >= NOALLOC_MAX_DEVICES) return fail("aotk_init: device %d beyond the supported %d", device, NOALLOC_MAX_DEVICES);
     HIPC(hipSetDevice(device));
     HIPC(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     g_device = device;
@@ -100,9 +101,14 @@ int aotk_init(int device) {
     // stream launches (for kernel traces that list every launch)
     const char *ng = getenv("AOTK_NO_GRAPH");
     g_decode_graphs = !(ng && ng[0] && ng[0] != '0');
-    if (device >= NOALLOC_MAX_DEVICES) return fail("aotk_init: device %d beyond the supported %d", device, NOALLOC_MAX_DEVICES);
     void *na = nullptr;
-    HIPC(hipGetSymbolAddress(&na, HIP_SYMBOL(scratch)));
+    hipError_t e = hipGetSymbolAddress(&na, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !na) {
+        // leave the library uninitialised so that a later call retries
+        (void)hipStreamDestroy(g_stream);
+        g_stream = nullptr;
+        return fail("aotk_init: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    }
     g_noalloc_scratch[device] = na;
     return 0;
 }
@@ -679,29 +685,40 @@ aotk_model *aotk_model_load(const aotk_model_spec *spec, const void *blob_host, 
     ArenaMap map;
     aotk_model *m = model_alloc(spec, blob_len, map);
     if (!m) return nullptr;
-    // One upload of the whole tensor-data section, then an on-device repack.
+    // Tensor by tensor: each matrix is uploaded into one staging buffer sized
+    // to the largest matrix (not the whole blob, so that loading needs the
+    // model's HBM plus one tensor) and repacked from there; vectors go
+    // straight to their place. The stream orders each upload after the
+    // previous repack.
+    size_t max_len = 0;
+    for_each_tensor(spec, [&](const aotk_tensor &t, uint32_t, bool matrix, bool) {
+        if (matrix && t.len > max_len) max_len = t.len;
+        return 0;
+    });
     uint8_t *staging = nullptr;
-    if (hipMalloc(&staging, blob_len) != hipSuccess || hipMemcpyAsync(staging, blob_host, blob_len, hipMemcpyHostToDevice, g_stream) != hipSuccess) {
-        fail("uploading the %zu-byte blob failed", blob_len);
-        if (staging) (void)hipFree(staging);
+    if (hipMalloc(&staging, max_len ? max_len : 1) != hipSuccess) {
+        fail("hipMalloc of the %zu-byte upload buffer failed", max_len);
         (void)hipFree(m->arena);
         delete m;
         return nullptr;
     }
-    for_each_tensor(&m->spec, [&](const aotk_tensor &t, uint32_t, bool matrix, bool) {
+    const uint8_t *src = (const uint8_t *)blob_host;
+    int rc = for_each_tensor(&m->spec, [&](const aotk_tensor &t, uint32_t, bool matrix, bool) {
         uint8_t *dst = m->arena + map.find(t.off);
         if (matrix) {
+            if (hipMemcpyAsync(staging, src + t.off, t.len, hipMemcpyHostToDevice, g_stream) != hipSuccess)
+                return fail("uploading a %zu-byte tensor failed", (size_t)t.len);
             DevWeight w = dev_weight(m, map, t);
-            launch_repack(w, staging + t.off, g_stream);
-        } else {
-            (void)hipMemcpyAsync(dst, staging + t.off, t.rows * t.cols * 4, hipMemcpyDeviceToDevice, g_stream);
+            launch_repack(w, staging, g_stream);
+        } else if (hipMemcpyAsync(dst, src + t.off, t.rows * t.cols * 4, hipMemcpyHostToDevice, g_stream) != hipSuccess) {
+            return fail("uploading a %zu-value vector failed", (size_t)(t.rows * t.cols));
         }
         return 0;
     });
     hipError_t e = hipStreamSynchronize(g_stream);
     (void)hipFree(staging);
-    if (e != hipSuccess) {
-        fail("weight repack failed: %s", hipGetErrorString(e));
+    if (rc || e != hipSuccess) {
+        if (!rc) fail("weight repack failed: %s", hipGetErrorString(e));
         (void)hipFree(m->arena);
         delete m;
         return nullptr;
@@ -834,7 +851,7 @@ struct aotk_state {
     float *am_ws;
     uint32_t *ctl;     // [0] token, [1] pos, [2] argmax / sampled, [3] generated count, [4] sampler window count
     uint32_t *tokens;  // [max_batch]
-    uint32_t *hist;    // [ctx]
+    uint32_t *hist;    // [ctx + 1]: a generation from position 0 emits up to ctx + 1 tokens
     uint32_t *ctl_host;  // pinned staging for the control words
     std::vector<void *> allocs;
     // One greedy generation step (argmax, advance, decode step, position
@@ -946,7 +963,7 @@ aotk_state *aotk_state_new(aotk_model *m, size_t ctx, size_t max_batch) {
     st->am_ws = F(1024);
     st->ctl = (uint32_t *)alloc(64);
     st->tokens = (uint32_t *)alloc(B * 4);
-    st->hist = (uint32_t *)alloc(ctx * 4);
+    st->hist = (uint32_t *)alloc((ctx + 1) * 4);
     st->swin = (uint32_t *)alloc((ctx + SAMP_WIN_EXTRA + 1) * 4);
     st->samp_ws = (uint64_t *)alloc(sampler_scratch_bytes(d.vocab));
     ok = ok && st->attn_ws && st->ctl && st->tokens && st->hist && st->swin && st->samp_ws;
@@ -1487,6 +1504,71 @@ int aotk_time_matmul(const aotk_weight *const *ws, size_t n_w, const float *xs_d
     HIPC(hipEventCreate(&e1));
     HIPC(hipEventRecord(e0, g_stream));
     for (size_t it = 0; it < iters; it++) launch_matvec(ws[it % n_w]->dw, act, m, y, nullptr, g_stream);
+    HIPC(hipEventRecord(e1, g_stream));
+    HIPC(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    HIPC(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    HIPC(hipGetLastError());
+    *ms_per_launch = ms / (float)iters;
+    return 0;
+}
+
+}  // extern "C"
+
+// HBM ceiling probes. Each thread moves HBM_V 16-byte vectors (all loads
+// issued before any use), one thread per HBM_V * 16 bytes, no grid-stride
+// loop: a plain streaming launch of the size under test. The read probe folds
+// what it loaded into one word and stores it only when it equals a value the
+// data never produces, so the loads cannot be dropped and nothing is written.
+constexpr int HBM_V = 4;
+__global__ __launch_bounds__(256) void k_hbm_read(const uint4 *src, size_t n16, uint32_t *sink) {
+    const size_t base = ((size_t)blockIdx.x * 256 + threadIdx.x) * HBM_V;
+    uint4 v[HBM_V];
+#pragma unroll
+    for (int k = 0; k < HBM_V; k++) v[k] = base + k < n16 ? src[base + k] : make_uint4(0, 0, 0, 0);
+    uint32_t acc = 0;
+#pragma unroll
+    for (int k = 0; k < HBM_V; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    if (acc == 0x9E3779B9u && base == 0) sink[0] = acc;
+}
+__global__ __launch_bounds__(256) void k_hbm_copy(uint4 *dst, const uint4 *src, size_t n16) {
+    const size_t base = ((size_t)blockIdx.x * 256 + threadIdx.x) * HBM_V;
+    uint4 v[HBM_V];
+#pragma unroll
+    for (int k = 0; k < HBM_V; k++)
+        if (base + k < n16) v[k] = src[base + k];
+#pragma unroll
+    for (int k = 0; k < HBM_V; k++)
+        if (base + k < n16) dst[base + k] = v[k];
+}
+
+extern "C" {
+
+int aotk_time_hbm(int copy, void *const *bufs, size_t n_bufs, size_t bytes, size_t iters, float *ms_per_launch) {
+    if (ensure_init()) return -1;
+    if (!bufs || n_bufs < (copy ? 2u : 1u) || iters == 0 || bytes < 16 || bytes % 16)
+        return fail("time_hbm: need %s buffer(s), iters > 0 and a size that is a multiple of 16 bytes", copy ? "2+" : "1+");
+    for (size_t i = 0; i < n_bufs; i++)
+        if (!bufs[i] || ((uintptr_t)bufs[i] & 15)) return fail("time_hbm: buffer %zu is null or not 16-byte aligned", i);
+    const size_t n16 = bytes / 16;
+    const size_t blocks = (n16 + 256 * HBM_V - 1) / (256 * HBM_V);
+    if (blocks > 0x7fffffffu) return fail("time_hbm: %zu bytes is too large", bytes);
+    uint32_t *sink = (uint32_t *)lib_scratch(256);
+    if (!sink) return -1;
+    auto one = [&](size_t it) {
+        if (copy)
+            k_hbm_copy<<<(unsigned)blocks, 256, 0, g_stream>>>((uint4 *)bufs[(it + 1) % n_bufs], (const uint4 *)bufs[it % n_bufs], n16);
+        else
+            k_hbm_read<<<(unsigned)blocks, 256, 0, g_stream>>>((const uint4 *)bufs[it % n_bufs], n16, sink);
+    };
+    one(0);  // warm-up
+    hipEvent_t e0, e1;
+    HIPC(hipEventCreate(&e0));
+    HIPC(hipEventCreate(&e1));
+    HIPC(hipEventRecord(e0, g_stream));
+    for (size_t it = 0; it < iters; it++) one(it);
     HIPC(hipEventRecord(e1, g_stream));
     HIPC(hipEventSynchronize(e1));
     float ms = 0.0f;

@@ -20,10 +20,21 @@ Also reported on the same JSON line:
   matvec_kinds   the same for the other seven kinds at every shape
   roofline       the dominant decode kernel (Q4_K matvec, 14336x4096) vs
                  MI355X HBM peak, timed with HIP events on the library stream
-  other_configs  Qwen3-8B Q8_0 (4096-token prefill, then 256 decode tokens) and
-                 Gemma-3-4B Q5_K_M (8192-token prefill, then 256 decode tokens)
+  prompt_hbm_frac
+                 the prompt's binding roof at 64-token chunks: every chunk
+                 streams the layer weights once, bytes / prompt time / 8 TB/s
+  decode_hbm_frac
+                 (weights + attended KV rows) per token x tok/s / 8 TB/s
+  hbm_ceiling    this box's measured streaming ceilings (read-only probe at
+                 the matvec's 33 MB and at 1 GiB, a 256 MiB copy kernel)
+  other_configs  TinyLlama-1.1B Q4_K_M (configs[0]: 6-token prompt, 32
+                 greedy tokens), Qwen3-8B Q8_0 (4096-token prefill, then 256
+                 decode tokens) and Gemma-3-4B Q5_K_M (8192-token prefill,
+                 then 256 decode tokens), each with HBM fractions
   cpu_baseline   the CPU oracle (restated avx2+f16c reference kernels) on a
-                 bounded sample of the same workload on this host's cores
+                 bounded sample of the same workload on this host's cores,
+                 plus the configs[1] matvec cells and bounded decode samples
+                 of the Qwen3 / Gemma-3 configs on the host
 
   python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--no-cpu]
 """
@@ -61,6 +72,115 @@ def matvec_bytes(kind, rows, cols):
     return rows * abi.row_bytes(kind, cols) + abi.act_bytes(kind, cols) + 4 * rows
 
 
+def layer_weight_bytes(spec):
+    """Bytes of every layer matrix (what one prompt chunk streams once)."""
+    return sum(getattr(spec.layers[i], n).len for i in range(spec.d["n_layer"])
+               for n in ("wq", "wk", "wv", "wo", "gate", "up", "down"))
+
+
+def kv_bytes_per_token(spec, first, n):
+    """Mean KV-cache bytes one decode step reads (K and V rows of every
+    attended position, f32) over decode positions first..first+n-1; local
+    layers of a sliding-window model attend min(pos + 1, window) positions
+    (window_start, crates/aot-kernels/src/ops.rs:171-177)."""
+    d = spec.d
+    kv_row = 2 * d["n_kv_head"] * d["head_dim"] * 4
+    win = int(spec.spec.dims.swa_window)
+    total = 0
+    for li in range(d["n_layer"]):
+        local = spec.layers[li].local_attn and win > 0
+        for p in range(first, first + n):
+            total += (min(p + 1, win) if local else p + 1) * kv_row
+    return total / max(n, 1)
+
+
+def hbm_ceiling(aotk):
+    """The box's own streaming ceilings beside the 8 TB/s spec: a read-only
+    probe over the Q4_K 14336x4096 matvec's 33 MB (rotated past 1 GB, the
+    matvec's own launch size) and over 1 GiB, and a copy kernel over 256 MiB
+    (read + write counted)."""
+    out = {}
+    small = 33_030_144  # 14336 x 4096 Q4_K weight bytes, rounded to 16
+    bufs = [aotk.DeviceBuffer(small) for _ in range(32)]
+    ms = aotk.time_hbm(bufs, small, 320)
+    out["read_33MB_GBs"] = round(small / (ms * 1e-3) / 1e9, 1)
+    out["read_33MB_us"] = round(ms * 1e3, 2)
+    for b in bufs:
+        b.free()
+    big = 1 << 30
+    bufs = [aotk.DeviceBuffer(big) for _ in range(2)]
+    ms = aotk.time_hbm(bufs, big, 20)
+    out["read_1GiB_GBs"] = round(big / (ms * 1e-3) / 1e9, 1)
+    q = 256 << 20
+    ms = aotk.time_hbm(bufs, q, 20, copy=True)
+    out["copy_256MiB_GBs"] = round(2 * q / (ms * 1e-3) / 1e9, 1)
+    for b in bufs:
+        b.free()
+    out["peak_GBs"] = HBM_PEAK_GBS
+    out["note"] = "k_hbm_read / k_hbm_copy (aotk_time_hbm): 4 x 16-byte loads per lane, one lane per 64 bytes, HIP events"
+    return out
+
+
+def cpu_matvec_cells(aotk, shapes, kinds, budget_s=0.25):
+    """configs[1] on the host: the oracle's avx2 matvec (matvec.rs:358-401
+    drivers) for every kind and shape, the same 512 distinct device-encoded
+    rows tiled to the full shape as the GPU cells, min(cores, 8) threads;
+    GB/s of the same algorithmic bytes."""
+    import numpy as np
+    from oracle import oracle as O
+    from aotk import abi
+    threads = min(os.cpu_count() or 1, 8)
+    pool = O.Pool(threads)
+    out = {}
+    for kind in kinds:
+        cells = {}
+        for rows, cols in shapes:
+            rng = np.random.default_rng(1)
+            base = aotk.quantize_rows(kind, (rng.standard_normal((min(rows, 512), cols)) * 0.02).astype(np.float32))
+            w = np.resize(base, (rows, base.shape[1]))
+            xa = O.quantize_act(kind, rng.standard_normal(cols).astype(np.float32))
+            O.matvec(kind, w, xa, rows, cols, pool)  # warm-up (page-in)
+            n, t = 0, time.perf_counter()
+            while n < 2 or time.perf_counter() - t < budget_s:
+                O.matvec(kind, w, xa, rows, cols, pool)
+                n += 1
+            dt = (time.perf_counter() - t) / n
+            cells[f"{rows}x{cols}"] = round(matvec_bytes(kind, rows, cols) / dt / 1e9, 2)
+            del w
+        out[abi.KIND_NAMES[kind]] = cells
+    return dict(GBs=out, threads=threads, kind="port", note="oracle avx2+f16c matvec per call, GB/s of the algorithmic bytes")
+
+
+def cpu_decode_from_gpu_kv(spec, blob, st, n_ctx, first_tok, budget_s):
+    """A bounded CPU sample of a long-context decode: the GPU's prefilled KV
+    rows (bit-identical to the oracle's prefill, which the stream tests pin)
+    copied into the oracle, then greedy decode forwards from n_ctx on
+    min(cores, 8) threads until the budget is spent."""
+    import numpy as np
+    from oracle import oracle as O
+    d = spec.d
+    kvd = d["n_kv_head"] * d["head_dim"]
+    threads = min(os.cpu_count() or 1, 8)
+    ctx = n_ctx + 64
+    k, v = st.kv_download(n_ctx)
+    m = O.Model(spec, blob, ctx, max_batch=1, n_threads=threads, kernels=1)
+    rk, rv = m.kv(ctx)
+    rk.reshape(d["n_layer"], ctx, kvd)[:, :n_ctx] = k.reshape(d["n_layer"], n_ctx, kvd)
+    rv.reshape(d["n_layer"], ctx, kvd)[:, :n_ctx] = v.reshape(d["n_layer"], n_ctx, kvd)
+    del k, v
+    tok, pos, n = first_tok, n_ctx, 0
+    t = time.perf_counter()
+    while (n < 2 or time.perf_counter() - t < budget_s) and n < 60:
+        m.forward(tok, pos, True)
+        tok = O.argmax(m.logits())
+        pos += 1
+        n += 1
+    dt = time.perf_counter() - t
+    m.close()
+    return dict(decode_tok_s=round(n / dt, 3), threads=threads, kind="port",
+                sample=f"{n} greedy decode forwards at positions {n_ctx}..{n_ctx + n - 1} on the GPU-prefilled KV")
+
+
 def time_kernel(aotk, kind, rows, cols, iters=200, min_bytes=1 << 30):
     """Mean ms per launch of the matvec over rotated synthetic copies."""
     import numpy as np
@@ -83,11 +203,13 @@ def time_kernel(aotk, kind, rows, cols, iters=200, min_bytes=1 << 30):
     return ms, copies
 
 
-def extra_config(aotk, configs, name, n_ctx, steps, chunk=64):
+def extra_config(aotk, configs, name, n_ctx, steps, chunk=64, cpu_s=0.0):
     """Another benchmark config as written: the KV cache prefilled by a
     random-id prompt of n_ctx tokens through the batched prompt path
     (app.rs:474-485, chunks of 64; timed: prefill tok/s), then `steps`
-    greedy decode forwards (timed: decode tok/s)."""
+    greedy decode forwards (timed: decode tok/s). HBM fractions count the
+    weights plus the attended KV rows per token against the 8 TB/s peak; the
+    prefill's counts every chunk's pass over the layer weights."""
     spec = configs.build(name)
     model = aotk.Model(spec, seed=SEED)
     st = aotk.State(model, n_ctx + steps + 2, chunk)
@@ -104,11 +226,57 @@ def extra_config(aotk, configs, name, n_ctx, steps, chunk=64):
     aotk.sync()
     dt = time.perf_counter() - t
     wb = model.weight_bytes()
+    kvb = kv_bytes_per_token(spec, n_ctx, steps)
+    tok_s = steps / dt
+    pre_b = -(-n_ctx // chunk) * layer_weight_bytes(spec) + spec.out_tensor.len
+    res = dict(decode_tok_s=round(tok_s, 2), prefill_tok_s=round(n_ctx / t_pre, 1), prefill_s=round(t_pre, 3),
+               context=n_ctx, steps=steps, weight_GB=round(wb / 1e9, 3), kv_GB_per_token=round(kvb / 1e9, 4),
+               decode_hbm_GBs=round((wb + kvb) * tok_s / 1e9, 1),
+               decode_hbm_frac=round((wb + kvb) * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+               prefill_hbm_frac=round(pre_b / t_pre / 1e9 / HBM_PEAK_GBS, 4), greedy_head=gen[:4],
+               note=f"{n_ctx}-token random-id prompt in {chunk}-token chunks, then {steps} greedy decode tokens")
+    if cpu_s > 0:
+        blob = model.download()
+        res["cpu_baseline"] = cpu_decode_from_gpu_kv(spec, blob, st, n_ctx, gen[0], cpu_s)
+        del blob
     st.free()
     model.free()
-    return dict(decode_tok_s=round(steps / dt, 2), prefill_tok_s=round(n_ctx / t_pre, 1), prefill_s=round(t_pre, 3),
-                context=n_ctx, steps=steps, weight_GB=round(wb / 1e9, 3), greedy_head=gen[:4],
-                note=f"{n_ctx}-token random-id prompt in {chunk}-token chunks, then {steps} greedy decode tokens")
+    return res
+
+
+def tinyllama_config(aotk, configs, reps=20):
+    """configs[0] as written: TinyLlama-1.1B shape Q4_K_M, a 6-token
+    random-id prompt (batch 1 forward_batch), then 32 greedy tokens (31
+    forwards). The config is milliseconds long, so it runs `reps` times
+    (same positions, the KV rows rewritten) and the median is reported."""
+    import statistics
+    name = "tinyllama-1.1b-q4km"
+    spec = configs.build(name)
+    model = aotk.Model(spec, seed=SEED)
+    st = aotk.State(model, 6 + 32, 64)
+    toks = configs.prompt_tokens(1, 6, spec.d["vocab"])
+    st.prompt(toks, batch=64)
+    st.generate(6, 32)  # warm-up and graph capture
+    tp, tg = [], []
+    for _ in range(reps):
+        aotk.sync()
+        t = time.perf_counter()
+        st.prompt(toks, batch=64)
+        aotk.sync()
+        tp.append(time.perf_counter() - t)
+        t = time.perf_counter()
+        gen = st.generate(6, 32)
+        aotk.sync()
+        tg.append(time.perf_counter() - t)
+    wb = model.weight_bytes()
+    kvb = kv_bytes_per_token(spec, 6, 31)
+    tok_s = 31 / statistics.median(tg)
+    st.free()
+    model.free()
+    return dict(prompt_tok_s=round(6 / statistics.median(tp), 1), decode_tok_s=round(tok_s, 1),
+                weight_GB=round(wb / 1e9, 4), decode_hbm_GBs=round((wb + kvb) * tok_s / 1e9, 1),
+                decode_hbm_frac=round((wb + kvb) * tok_s / 1e9 / HBM_PEAK_GBS, 4), greedy_head=gen[:8],
+                note=f"6-token random-id prompt, then 32 greedy tokens (31 forwards); median of {reps} runs")
 
 
 def measured_traffic(kernel):
@@ -194,6 +362,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--extra-steps", type=int, default=256, help="decode tokens of the Qwen3 / Gemma-3 lines")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-extra-seconds", type=float, default=8.0,
+                    help="CPU decode sample per long-context config (0: none)")
     ap.add_argument("--no-micro", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the Qwen3 / Gemma-3 decode lines")
     ap.add_argument("--micro-only", action="store_true",
@@ -246,6 +416,11 @@ def main():
     log(f"decode: {a.steps} forwards in {t_gen * 1e3:.1f} ms ({tok_s:.1f} tok/s, "
         f"{wbytes * tok_s / 1e9:.0f} GB/s of weights)")
 
+    n_chunks = -(-a.prompt // a.chunk)
+    prompt_bytes = n_chunks * layer_weight_bytes(spec) + spec.out_tensor.len
+    prompt_hbm_frac = prompt_bytes / t_prompt / 1e9 / HBM_PEAK_GBS
+    kvb = kv_bytes_per_token(spec, a.prompt + a.warmup, a.steps)
+    ceiling = None if a.no_micro else hbm_ceiling(aotk)
     roofline = None
     micro = {}
     kinds_micro = {}
@@ -268,12 +443,17 @@ def main():
         roofline = dict(bound="hbm", achieved=dom["GBs"], peak=HBM_PEAK_GBS, unit="GB/s", frac=dom["frac"],
                         traffic=measured_traffic("k_mv_kq<Q4_K> 14336x4096"),
                         kernel="k_mv_kq<Q4_K> 14336x4096 (ffn gate/up shape)",
-                        bytes_per_launch=matvec_bytes(abi.Q4_K, 14336, 4096), us_per_launch=dom["us"])
+                        bytes_per_launch=matvec_bytes(abi.Q4_K, 14336, 4096), us_per_launch=dom["us"],
+                        frac_of_read_ceiling=round(dom["GBs"] / ceiling["read_33MB_GBs"], 4))
 
     extra = {}
     if not a.no_extra:
+        extra["tinyllama-1.1b-q4km"] = tinyllama_config(aotk, configs)
+        log(f"tinyllama-1.1b-q4km: prompt {extra['tinyllama-1.1b-q4km']['prompt_tok_s']} tok/s, "
+            f"decode {extra['tinyllama-1.1b-q4km']['decode_tok_s']} tok/s")
         for name, n_ctx in (("qwen3-8b-q8_0", 4096), ("gemma3-4b-q5km", 8192)):
-            extra[name] = extra_config(aotk, configs, name, n_ctx, a.extra_steps)
+            extra[name] = extra_config(aotk, configs, name, n_ctx, a.extra_steps,
+                                       cpu_s=0.0 if a.no_cpu else a.cpu_extra_seconds)
             log(f"{name}: prefill {n_ctx} tokens {extra[name]['prefill_tok_s']} tok/s, "
                 f"{extra[name]['decode_tok_s']} tok/s decode at {n_ctx}+ context")
 
@@ -284,6 +464,12 @@ def main():
         st.free()
         cpu = cpu_baseline(spec, blob, a.prompt, a.chunk, a.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads ({cpu['host_cpu']})")
+        if not a.no_micro:
+            cpu["matvec"] = cpu_matvec_cells(aotk, [(4096, 4096), (14336, 4096), (4096, 14336), (128256, 4096)],
+                                             (abi.Q4_K, abi.Q6_K, abi.Q5_K, abi.Q8_0, abi.Q4_0, abi.Q5_0, abi.F16,
+                                              abi.BF16))
+            log(f"cpu matvec GB/s: {cpu['matvec']['GBs']}")
+        cpu["other_configs"] = {k: v.get("cpu_baseline") for k, v in extra.items() if v.get("cpu_baseline")}
 
     line = {
         "metric": "decode tok/s + Q4_K matvec HBM GB/s (frac of peak); prompt tok/s, 1 MI355X",
@@ -304,6 +490,11 @@ def main():
         "prompt_tok_s": round(prompt_tok_s, 2),
         "prompt_int8_TOPs": round(prompt_tops, 1),
         "prompt_int8_frac": round(prompt_tops / INT8_PEAK_TOPS, 4),
+        "prompt_hbm_frac": round(prompt_hbm_frac, 4),
+        "prompt_hbm_bytes": prompt_bytes,
+        "decode_kv_bytes_per_token": round(kvb),
+        "decode_hbm_frac": round((wbytes + kvb) * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+        "hbm_ceiling": ceiling,
         "decode_weight_bytes_per_token": wbytes,
         "decode_weight_GBs": round(wbytes * tok_s / 1e9, 1),
         "q4k_matvec": micro,

@@ -356,6 +356,14 @@ int aotk_time_matvec(const aotk_weight *const *ws, size_t n_w, const float *x_de
 int aotk_time_matmul(const aotk_weight *const *ws, size_t n_w, const float *xs_dev, size_t m, size_t iters,
                      float *ms_per_launch);
 
+/* Measurement helper, no reference counterpart (the HBM ceiling that the
+ * matvec fractions are read against): `iters` launches of a streaming probe
+ * over `bytes` bytes, rotating over the n_bufs device buffers (16-byte
+ * aligned): copy == 0 reads bufs[i] (nothing written), copy != 0 copies
+ * bufs[i] to bufs[i + 1]. Writes the mean ms per launch (HIP events on the
+ * library stream). */
+int aotk_time_hbm(int copy, void *const *bufs, size_t n_bufs, size_t bytes, size_t iters, float *ms_per_launch);
+
 /* The library's HIP stream (hipStream_t) for callers that time on it. */
 void *aotk_stream(void);
 

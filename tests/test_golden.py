@@ -75,3 +75,37 @@ def test_gpu_matches_model_fixture(aotk, name):
     st.prompt([int(t) for t in f["prompt"]], batch=8)
     assert np.array_equal(st.logits().view(np.uint32), f["logits"].view(np.uint32))
     assert st.generate(6, 16) == [int(t) for t in f["greedy"]]
+
+
+STREAMS = {"tinyllama-1.1b-q4km": (1, 6, 32), "llama3-8b-q4km": (1, 512, 128),
+           "qwen3-8b-q8_0": (2, 4096, 256), "gemma3-4b-q5km": (2, 8192, 256)}
+
+
+@pytest.mark.parametrize("name", list(STREAMS))
+def test_stream_fixture_shape(name):
+    """The full-length stream fixtures hold the config's own prompt (the
+    seeded splitmix64 ids bench.py uses) and stream length."""
+    from aotk import configs
+    seed, n_prompt, n_gen = STREAMS[name]
+    f = load(f"stream_{name}.npz")
+    vocab = configs.build(name).d["vocab"]
+    assert f["prompt"].tolist() == configs.prompt_tokens(seed, n_prompt, vocab)
+    assert f["greedy"].shape == (n_gen,) and int(f["greedy"].max()) < vocab
+    assert int(f["chunk"]) == 64 and f["prompt_sha256"].shape == (32,)
+
+
+def test_oracle_reproduces_tinyllama_stream(oracle):
+    """configs[0] is small enough to recompute here: the oracle still
+    writes the committed stream and logits digests."""
+    import hashlib
+    from aotk import configs
+    f = load("stream_tinyllama-1.1b-q4km.npz")
+    spec = configs.build("tinyllama-1.1b-q4km")
+    blob = oracle.synth_blob(spec, 0x5EED)
+    m = oracle.Model(spec, blob, 38, max_batch=64, n_threads=8)
+    m.prompt([int(t) for t in f["prompt"]], batch=64)
+    sha = lambda a: np.frombuffer(hashlib.sha256(a.tobytes()).digest(), np.uint8)  # noqa: E731
+    assert np.array_equal(sha(m.logits()), f["prompt_sha256"])
+    assert m.generate(6, 32) == f["greedy"].tolist()
+    assert np.array_equal(sha(m.logits()), f["final_sha256"])
+    m.close()

@@ -291,7 +291,12 @@ def _or_rmsnorm(oracle, x, w):
     return out
 
 
-@pytest.mark.parametrize("hd,nh,nkv,window", [(64, 32, 4, 0), (128, 32, 8, 0), (256, 8, 4, 5), (128, 4, 4, 0), (64, 8, 2, 7), (128, 8, 8, 90)])
+@pytest.mark.parametrize("hd,nh,nkv,window", [
+    (64, 32, 4, 0), (128, 32, 8, 0), (256, 8, 4, 5), (128, 4, 4, 0), (64, 8, 2, 7), (128, 8, 8, 90),
+    # every query-heads-per-kv-head ratio at head_dim 256 (1, 2, 4, 8 take the
+    # batched-rows scores kernel, 3 and 6 the generic one) and ratio 3 at 64 / 128
+    (256, 4, 4, 0), (256, 8, 2, 0), (256, 8, 1, 3), (256, 6, 2, 0), (256, 12, 2, 9),
+    (128, 6, 2, 0), (64, 12, 4, 0)])
 def test_attention(aotk, oracle, hd, nh, nkv, window):
     rng = np.random.default_rng(hd + nh)
     ctx, layer = 150, 1
