@@ -164,7 +164,7 @@ def load(path=None):
     _sig(lib, "aotk_prefix_load", i, [vp, vp, sz, C.POINTER(u32), sz, C.POINTER(sz), C.POINTER(sz)])
     _sig(lib, "aotk_stream", vp, [])
     _sig(lib, "aotk_time_matvec", i, [C.POINTER(vp), sz, vp, sz, C.POINTER(C.c_float)])
-    _sig(lib, "aotk_time_hbm", i, [C.c_int, C.POINTER(vp), sz, sz, sz, C.POINTER(C.c_float)])
+    _sig(lib, "aotk_time_hbm", i, [C.c_int, C.c_int, C.POINTER(vp), sz, sz, sz, C.POINTER(C.c_float)])
     _sig(lib, "aotk_time_matmul", i, [C.POINTER(vp), sz, vp, sz, sz, C.POINTER(C.c_float)])
     _lib = lib
     return lib

@@ -96,14 +96,14 @@ class Weight:
             pass
 
 
-def time_hbm(buffers, nbytes, iters, copy=False):
+def time_hbm(buffers, nbytes, iters, copy=False, loads_per_lane=4):
     """Mean ms per launch of the HBM probe (read-only, or a copy from each
     buffer to the next) over `nbytes` of the DeviceBuffers in turn."""
     arr = (C.c_void_p * len(buffers))(*[b.ptr for b in buffers])
     for b in buffers:
         assert nbytes <= b.nbytes
     ms = C.c_float()
-    abi.check(_lib().aotk_time_hbm(1 if copy else 0, arr, len(buffers), int(nbytes), int(iters), C.byref(ms)))
+    abi.check(_lib().aotk_time_hbm(1 if copy else 0, int(loads_per_lane), arr, len(buffers), int(nbytes), int(iters), C.byref(ms)))
     return ms.value
 
 

@@ -1517,51 +1517,71 @@ int aotk_time_matmul(const aotk_weight *const *ws, size_t n_w, const float *xs_d
 
 }  // extern "C"
 
-// HBM ceiling probes. Each thread moves HBM_V 16-byte vectors (all loads
-// issued before any use), one thread per HBM_V * 16 bytes, no grid-stride
-// loop: a plain streaming launch of the size under test. The read probe folds
-// what it loaded into one word and stores it only when it equals a value the
-// data never produces, so the loads cannot be dropped and nothing is written.
-constexpr int HBM_V = 4;
+// HBM ceiling probes: a plain streaming launch of the size under test, no
+// grid-stride loop. A block of 256 lanes moves HBM_V * 4 KB: load k of lane t
+// reads vector k * 256 + t of the block's range, so every load instruction
+// is 1 KB contiguous per wave, and all HBM_V loads are issued before any
+// use (HBM_V = 1, 2, 4 or 8 loads in flight per lane). The read probe folds what it loaded into one word and stores it only
+// when it equals a value the data never produces, so the loads cannot be
+// dropped and nothing is written.
+template <int HBM_V>
 __global__ __launch_bounds__(256) void k_hbm_read(const uint4 *src, size_t n16, uint32_t *sink) {
-    const size_t base = ((size_t)blockIdx.x * 256 + threadIdx.x) * HBM_V;
+    const size_t base = (size_t)blockIdx.x * 256 * HBM_V + threadIdx.x;
     uint4 v[HBM_V];
 #pragma unroll
-    for (int k = 0; k < HBM_V; k++) v[k] = base + k < n16 ? src[base + k] : make_uint4(0, 0, 0, 0);
+    for (int k = 0; k < HBM_V; k++) v[k] = base + k * 256 < n16 ? src[base + k * 256] : make_uint4(0, 0, 0, 0);
     uint32_t acc = 0;
 #pragma unroll
     for (int k = 0; k < HBM_V; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
     if (acc == 0x9E3779B9u && base == 0) sink[0] = acc;
 }
+template <int HBM_V>
 __global__ __launch_bounds__(256) void k_hbm_copy(uint4 *dst, const uint4 *src, size_t n16) {
-    const size_t base = ((size_t)blockIdx.x * 256 + threadIdx.x) * HBM_V;
+    const size_t base = (size_t)blockIdx.x * 256 * HBM_V + threadIdx.x;
     uint4 v[HBM_V];
 #pragma unroll
     for (int k = 0; k < HBM_V; k++)
-        if (base + k < n16) v[k] = src[base + k];
+        if (base + k * 256 < n16) v[k] = src[base + k * 256];
 #pragma unroll
     for (int k = 0; k < HBM_V; k++)
-        if (base + k < n16) dst[base + k] = v[k];
+        if (base + k * 256 < n16) dst[base + k * 256] = v[k];
 }
 
 extern "C" {
 
-int aotk_time_hbm(int copy, void *const *bufs, size_t n_bufs, size_t bytes, size_t iters, float *ms_per_launch) {
+int aotk_time_hbm(int copy, int loads_per_lane, void *const *bufs, size_t n_bufs, size_t bytes, size_t iters,
+                  float *ms_per_launch) {
     if (ensure_init()) return -1;
+    const int U = loads_per_lane;
+    if (U != 1 && U != 2 && U != 4 && U != 8) return fail("time_hbm: loads_per_lane must be 1, 2, 4 or 8");
     if (!bufs || n_bufs < (copy ? 2u : 1u) || iters == 0 || bytes < 16 || bytes % 16)
         return fail("time_hbm: need %s buffer(s), iters > 0 and a size that is a multiple of 16 bytes", copy ? "2+" : "1+");
     for (size_t i = 0; i < n_bufs; i++)
         if (!bufs[i] || ((uintptr_t)bufs[i] & 15)) return fail("time_hbm: buffer %zu is null or not 16-byte aligned", i);
     const size_t n16 = bytes / 16;
-    const size_t blocks = (n16 + 256 * HBM_V - 1) / (256 * HBM_V);
+    const size_t blocks = (n16 + 256 * (size_t)U - 1) / (256 * (size_t)U);
     if (blocks > 0x7fffffffu) return fail("time_hbm: %zu bytes is too large", bytes);
     uint32_t *sink = (uint32_t *)lib_scratch(256);
     if (!sink) return -1;
     auto one = [&](size_t it) {
-        if (copy)
-            k_hbm_copy<<<(unsigned)blocks, 256, 0, g_stream>>>((uint4 *)bufs[(it + 1) % n_bufs], (const uint4 *)bufs[it % n_bufs], n16);
-        else
-            k_hbm_read<<<(unsigned)blocks, 256, 0, g_stream>>>((const uint4 *)bufs[it % n_bufs], n16, sink);
+        const unsigned g = (unsigned)blocks;
+        uint4 *d = (uint4 *)bufs[(it + 1) % n_bufs];
+        const uint4 *src = (const uint4 *)bufs[it % n_bufs];
+        if (copy) {
+            switch (U) {
+            case 1: k_hbm_copy<1><<<g, 256, 0, g_stream>>>(d, src, n16); break;
+            case 2: k_hbm_copy<2><<<g, 256, 0, g_stream>>>(d, src, n16); break;
+            case 4: k_hbm_copy<4><<<g, 256, 0, g_stream>>>(d, src, n16); break;
+            default: k_hbm_copy<8><<<g, 256, 0, g_stream>>>(d, src, n16); break;
+            }
+        } else {
+            switch (U) {
+            case 1: k_hbm_read<1><<<g, 256, 0, g_stream>>>(src, n16, sink); break;
+            case 2: k_hbm_read<2><<<g, 256, 0, g_stream>>>(src, n16, sink); break;
+            case 4: k_hbm_read<4><<<g, 256, 0, g_stream>>>(src, n16, sink); break;
+            default: k_hbm_read<8><<<g, 256, 0, g_stream>>>(src, n16, sink); break;
+            }
+        }
     };
     one(0);  // warm-up
     hipEvent_t e0, e1;

@@ -360,9 +360,11 @@ int aotk_time_matmul(const aotk_weight *const *ws, size_t n_w, const float *xs_d
  * matvec fractions are read against): `iters` launches of a streaming probe
  * over `bytes` bytes, rotating over the n_bufs device buffers (16-byte
  * aligned): copy == 0 reads bufs[i] (nothing written), copy != 0 copies
- * bufs[i] to bufs[i + 1]. Writes the mean ms per launch (HIP events on the
- * library stream). */
-int aotk_time_hbm(int copy, void *const *bufs, size_t n_bufs, size_t bytes, size_t iters, float *ms_per_launch);
+ * bufs[i] to bufs[i + 1]; loads_per_lane (1, 2, 4, 8) 16-byte loads in
+ * flight per lane, coalesced. Writes the mean ms per launch (HIP events on
+ * the library stream). */
+int aotk_time_hbm(int copy, int loads_per_lane, void *const *bufs, size_t n_bufs, size_t bytes, size_t iters,
+                  float *ms_per_launch);
 
 /* The library's HIP stream (hipStream_t) for callers that time on it. */
 void *aotk_stream(void);
