@@ -212,6 +212,7 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant4(const float *__restric
     const int n4 = n / 4;
     const int C = seq_chunk(n);
     const float4 *xr = (const float4 *)(x + m * n);
+    RMS_TS(0);
     float4 xv[KF], wv[KF];
 #pragma unroll
     for (int k = 0; k < KF; k++) {
@@ -234,7 +235,9 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant4(const float *__restric
         }
     }
     __syncthreads();
+    RMS_TS(1);
     const float ss = exact_seq_sum(sq, n, S);
+    RMS_TS(2);
     const float r = 1.0f / sqrtf(ss / (float)n + eps);
     const ActQ8K qk = q8k_row(out.q8k, m, n);
     const ActQ8_0 q0 = q80_row(out.q80, m, n);
@@ -247,6 +250,7 @@ __global__ __launch_bounds__(SEQ_T) void k_rmsnorm_quant4(const float *__restric
             quant256(v, lane, (size_t)(i >> 6), qk, q0);
         }
     }
+    RMS_TS(3);
 }
 
 void launch_rmsnorm_quant(const float *x, const float *w, size_t n, size_t m, float eps, RmsOut out, hipStream_t s) {
