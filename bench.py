@@ -344,9 +344,10 @@ def cpu_baseline(spec, blob, n_prompt, chunk, budget_s):
 
 
 def micro_only():
-    """Short program for counter runs: 200 launches of the Q4_K 14336x4096
-    matvec over rotated copies, then one device-to-device copy of 256 MiB
-    (the calibration kernel: it reads and writes exactly 256 MiB)."""
+    """Short program for counter and trace runs: 200 launches of the Q4_K
+    14336x4096 matvec over rotated copies, one device-to-device copy of 256
+    MiB (the calibration kernel: it reads and writes exactly 256 MiB), then
+    the HBM ceiling probes of the bench line."""
     import aotk
     from aotk import abi
     ms, copies = time_kernel(aotk, abi.Q4_K, 14336, 4096)
@@ -354,7 +355,10 @@ def micro_only():
     src, dst = aotk.DeviceBuffer(n), aotk.DeviceBuffer(n)
     aotk.copy_dev(dst, src, n)
     aotk.sync()
+    src.free()
+    dst.free()
     log(f"q4_K 14336x4096: {ms * 1e3:.2f} us over {copies} copies; copied {n} bytes")
+    log(f"hbm ceiling: {hbm_ceiling(aotk)}")
 
 
 def main():
