@@ -119,3 +119,24 @@ def test_e2e_models_bitexact(aotk, oracle, name):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"batch {batch}: rel L2 {rel_l2(a, b):.3g}"
         assert st.generate(n, 8) == ref.generate(n, 8)
         ref.close()
+
+
+def test_generate_fills_the_whole_context(aotk, oracle):
+    """A generation of ctx + 1 tokens from position 0 (forwards at every
+    position of the context) keeps all of its token history: the history
+    buffer holds ctx + 1 ids, and the stream equals the oracle's."""
+    from aotk import configs
+    spec = configs.build("tiny-llama")
+    blob = oracle.synth_blob(spec, 0x5EED)
+    ctx = 12
+    gm = aotk.Model(spec, blob)
+    st = aotk.State(gm, ctx)
+    ref = oracle.Model(spec, blob, ctx)
+    st.forward(5, 0, True)
+    ref.forward(5, 0, True)
+    got = st.generate(0, ctx + 1)
+    assert len(got) == ctx + 1
+    assert got == ref.generate(0, ctx + 1)
+    # one token more does not fit
+    with pytest.raises(aotk.AotkError):
+        st.generate(0, ctx + 2)
