@@ -288,7 +288,8 @@ int aotk_greedy(aotk_state *state, uint32_t *token_out);
 /* Greedy generation: starting from the current logits (after the prompt),
  * emit n tokens as app.rs:553-610 does with temperature 0 (sample, then feed
  * back unless it was the last), positions pos, pos+1, ... Writes the n
- * token ids to tokens_host. Device-resident loop: only token ids cross PCIe. */
+ * token ids to tokens_host. Device-resident loop: only token ids cross PCIe.
+ * The n - 1 forwards must fit the context: pos + n - 1 <= ctx, else -1. */
 int aotk_generate_greedy(aotk_state *state, size_t pos, size_t n, uint32_t *tokens_host);
 /* KV rows [0, n_pos) of every layer to / from the host, laid out as the
  * reference's cache: [n_layer][n_pos][kv_dim] f32 for K, then the same for V. */
