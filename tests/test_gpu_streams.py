@@ -61,3 +61,36 @@ def test_config_stream_full_length(aotk, name):
     finally:
         st.free()
         gm.free()
+
+
+@pytest.mark.gpu
+def test_prefix_continuation_at_config_scale(aotk):
+    """--save-kv / --load-kv (prefix.rs, app.rs:458-489) at the Qwen3-8B
+    config's size: 4095 prompt positions saved to an AOTP blob (1.2 GB),
+    loaded into a fresh state, the last prompt token evaluated there, then
+    256 greedy tokens: the stream and both logits digests equal the
+    uninterrupted run's fixture."""
+    from aotk import configs
+    f = _fixture("qwen3-8b-q8_0")
+    prompt = [int(t) for t in f["prompt"]]
+    want = [int(t) for t in f["greedy"]]
+    spec = configs.build("qwen3-8b-q8_0")
+    gm = aotk.Model(spec, seed=0x5EED)
+    ctx = len(prompt) + len(want)
+    a = aotk.State(gm, ctx, 64)
+    try:
+        a.prompt(prompt[:-1], batch=64)
+        blob = a.save_prefix(prompt, len(prompt) - 1)
+    finally:
+        a.free()
+    b = aotk.State(gm, ctx, 64)
+    try:
+        toks, nc = b.load_prefix(blob)
+        assert toks == prompt and nc == len(prompt) - 1
+        b.forward(prompt[-1], nc, True)
+        assert np.array_equal(_sha(b.logits()), f["prompt_sha256"])
+        assert b.generate(len(prompt), len(want)) == want
+        assert np.array_equal(_sha(b.logits()), f["final_sha256"])
+    finally:
+        b.free()
+        gm.free()
