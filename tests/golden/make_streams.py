@@ -20,6 +20,7 @@ tests/test_oracle.py and tests/test_oracle_forward.py; these fixtures freeze
 its outputs at lengths the GPU tests cannot afford to recompute on the CPU.
 
     python tests/golden/make_streams.py [config ...]
+    python tests/golden/make_streams.py --sampled [config ...]   (sampled_<config>.npz)
 """
 import hashlib
 import os
@@ -77,11 +78,37 @@ def stream(name, threads):
                 final_sha256=digest(lf), final_top_ids=fi, final_top_vals=fv)
 
 
+# Sampled streams (the app.rs:553-610 loop with sampler.rs): configs[0] and
+# configs[2] at their written lengths with --temp 0.8 --top-k 40 --top-p 0.95
+# --repeat-penalty 1.1 (window 64) and seed 42, the penalty window running
+# over the prompt and the generated tokens
+SAMPLED = {"tinyllama-1.1b-q4km": (1, 6, 32), "llama3-8b-q4km": (1, 512, 128)}
+SAMPLER = dict(temperature=0.8, top_k=40, top_p=0.95, repeat_penalty=1.1, repeat_last_n=64, seed=42)
+
+
+def sampled(name, threads):
+    pseed, n_prompt, n_gen = SAMPLED[name]
+    spec = configs.build(name)
+    blob = O.synth_blob(spec, SEED, n_threads=threads)
+    toks = configs.prompt_tokens(pseed, n_prompt, spec.d["vocab"])
+    m = O.Model(spec, blob, n_prompt + n_gen, max_batch=CHUNK, n_threads=threads)
+    m.prompt(toks, batch=CHUNK)
+    gen = m.generate_sampled(n_prompt, n_gen, O.Sampler(**SAMPLER), toks)
+    m.close()
+    print(f"{name} sampled: head {gen[:8]}", flush=True)
+    return dict(prompt=np.array(toks, np.uint32), sampled=np.array(gen, np.uint32), chunk=np.uint32(CHUNK),
+                **{k: np.float64(v) for k, v in SAMPLER.items()})
+
+
 def main():
     O.load()
-    names = sys.argv[1:] or list(STREAMS)
+    args = sys.argv[1:]
     threads = min(os.cpu_count() or 1, 8)
-    for name in names:
+    if args[:1] == ["--sampled"]:
+        for name in args[1:] or list(SAMPLED):
+            np.savez_compressed(os.path.join(HERE, f"sampled_{name}.npz"), **sampled(name, threads))
+        return
+    for name in args or list(STREAMS):
         np.savez_compressed(os.path.join(HERE, f"stream_{name}.npz"), **stream(name, threads))
 
 

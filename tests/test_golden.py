@@ -109,3 +109,26 @@ def test_oracle_reproduces_tinyllama_stream(oracle):
     assert m.generate(6, 32) == f["greedy"].tolist()
     assert np.array_equal(sha(m.logits()), f["final_sha256"])
     m.close()
+
+
+@pytest.mark.parametrize("name,seed,n_prompt,n_gen", [("tinyllama-1.1b-q4km", 1, 6, 32), ("llama3-8b-q4km", 1, 512, 128)])
+def test_sampled_fixture_shape(name, seed, n_prompt, n_gen):
+    from aotk import configs
+    f = load(f"sampled_{name}.npz")
+    vocab = configs.build(name).d["vocab"]
+    assert f["prompt"].tolist() == configs.prompt_tokens(seed, n_prompt, vocab)
+    assert f["sampled"].shape == (n_gen,) and int(f["sampled"].max()) < vocab
+    assert float(f["temperature"]) == 0.8 and int(f["top_k"]) == 40 and int(f["seed"]) == 42
+
+
+def test_oracle_reproduces_tinyllama_sampled_stream(oracle):
+    from aotk import configs
+    f = load("sampled_tinyllama-1.1b-q4km.npz")
+    spec = configs.build("tinyllama-1.1b-q4km")
+    blob = oracle.synth_blob(spec, 0x5EED)
+    m = oracle.Model(spec, blob, 38, max_batch=64, n_threads=8)
+    toks = [int(t) for t in f["prompt"]]
+    m.prompt(toks, batch=64)
+    cfg = dict(temperature=0.8, top_k=40, top_p=0.95, repeat_penalty=1.1, repeat_last_n=64, seed=42)
+    assert m.generate_sampled(6, 32, oracle.Sampler(**cfg), toks) == f["sampled"].tolist()
+    m.close()

@@ -94,3 +94,34 @@ def test_prefix_continuation_at_config_scale(aotk):
     finally:
         b.free()
         gm.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["tinyllama-1.1b-q4km", "llama3-8b-q4km"])
+def test_config_sampled_stream(aotk, name):
+    """The sampled loop (app.rs:553-610 with sampler.rs: temperature 0.8,
+    top-k 40, top-p 0.95, repeat penalty 1.1 over a 64-token window, seed
+    42) on the device at the config's written length, against the
+    oracle-written fixture (tests/golden/make_streams.py --sampled)."""
+    from aotk import configs
+    path = os.path.join(GOLDEN, f"sampled_{name}.npz")
+    if not os.path.exists(path):
+        pytest.fail(f"missing fixture {path}: run tests/golden/make_streams.py --sampled")
+    f = np.load(path)
+    prompt = [int(t) for t in f["prompt"]]
+    want = [int(t) for t in f["sampled"]]
+    cfg = dict(temperature=float(f["temperature"]), top_k=int(f["top_k"]), top_p=float(f["top_p"]),
+               repeat_penalty=float(f["repeat_penalty"]), repeat_last_n=int(f["repeat_last_n"]), seed=int(f["seed"]))
+    spec = configs.build(name)
+    gm = aotk.Model(spec, seed=0x5EED)
+    st = aotk.State(gm, len(prompt) + len(want), int(f["chunk"]))
+    sp = aotk.Sampler(**cfg)
+    try:
+        st.prompt(prompt, batch=int(f["chunk"]))
+        got = st.generate_sampled(sp, len(prompt), len(want), prompt)
+        first = next((i for i, (a, b) in enumerate(zip(got, want)) if a != b), None)
+        assert got == want, f"{name}: sampled streams part at token {first}"
+    finally:
+        sp.free()
+        st.free()
+        gm.free()
