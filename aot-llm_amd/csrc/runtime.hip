@@ -1521,9 +1521,10 @@ int aotk_time_matmul(const aotk_weight *const *ws, size_t n_w, const float *xs_d
 // grid-stride loop. A block of 256 lanes moves HBM_V * 4 KB: load k of lane t
 // reads vector k * 256 + t of the block's range, so every load instruction
 // is 1 KB contiguous per wave, and all HBM_V loads are issued before any
-// use (HBM_V = 1, 2, 4 or 8 loads in flight per lane). The read probe folds what it loaded into one word and stores it only
-// when it equals a value the data never produces, so the loads cannot be
-// dropped and nothing is written.
+// use (HBM_V = 1, 2, 4 or 8 loads in flight per lane). The read probe folds
+// what it loaded into one word and stores it (to the library scratch) only
+// when that word equals one constant, so the loads cannot be dropped and
+// nothing else is written.
 template <int HBM_V>
 __global__ __launch_bounds__(256) void k_hbm_read(const uint4 *src, size_t n16, uint32_t *sink) {
     const size_t base = (size_t)blockIdx.x * 256 * HBM_V + threadIdx.x;
