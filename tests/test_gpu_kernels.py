@@ -391,6 +391,36 @@ def test_exact_sequential_sum_rmsnorm(aotk, oracle, n):
     assert not bad, f"rows {bad} differ"
 
 
+@pytest.mark.parametrize("n", [2048, 2560, 4096])
+def test_exact_sequential_sum_fuzz(aotk, oracle, n):
+    """rmsnorm over 240 seeded rows of mixed scales, heavy tails, runs of
+    equal values and sparse zeros (the sums' binade crossings and .5 ties
+    fall at many different places): every row bit for bit."""
+    rng = np.random.default_rng(1000 + n)
+    rows = []
+    for i in range(240):
+        kind = i % 6
+        if kind == 0:
+            r = rng.standard_normal(n) * 10.0 ** rng.uniform(-4, 3)
+        elif kind == 1:
+            r = rng.standard_t(2, n)
+        elif kind == 2:
+            r = np.repeat(rng.standard_normal(n // 16), 16) * 2.0 ** rng.integers(-20, 10)
+        elif kind == 3:
+            r = np.where(rng.random(n) < 0.9, 0.0, rng.standard_normal(n))
+        elif kind == 4:
+            r = rng.integers(-8, 8, n) * 2.0 ** rng.integers(-12, 4)
+        else:
+            r = np.exp(rng.uniform(-15, 3, n)) * rng.choice([1, -1], n)
+        rows.append(r)
+    x = np.array(rows, np.float32)
+    w = np.ones(n, np.float32)
+    got = aotk.rmsnorm(x, w, 1e-5)
+    ref = np.stack([_or_rmsnorm(oracle, r, w) for r in x])
+    bad = [i for i in range(len(x)) if not np.array_equal(got[i].view(np.uint32), ref[i].view(np.uint32))]
+    assert not bad, f"rows {bad[:10]} differ"
+
+
 @pytest.mark.parametrize("n", [7, 64, 1000, 4096, 8192, 9000])
 def test_exact_sequential_sum_softmax(aotk, oracle, n):
     rng = np.random.default_rng(n + 1)
