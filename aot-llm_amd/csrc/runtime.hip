@@ -1524,13 +1524,18 @@ int aotk_time_matmul(const aotk_weight *const *ws, size_t n_w, const float *xs_d
 // use (HBM_V = 1, 2, 4 or 8 loads in flight per lane). The read probe folds
 // what it loaded into one word and stores it (to the library scratch) only
 // when that word equals one constant, so the loads cannot be dropped and
-// nothing else is written.
+// nothing else is written. Its loads carry the nontemporal hint, as the
+// decode matvecs' weight loads do (cold 33 MB reads 6.86 -> 6.68 us).
+typedef unsigned hbm_u4 __attribute__((ext_vector_type(4)));
 template <int HBM_V>
 __global__ __launch_bounds__(256) void k_hbm_read(const uint4 *src, size_t n16, uint32_t *sink) {
     const size_t base = (size_t)blockIdx.x * 256 * HBM_V + threadIdx.x;
     uint4 v[HBM_V];
 #pragma unroll
-    for (int k = 0; k < HBM_V; k++) v[k] = base + k * 256 < n16 ? src[base + k * 256] : make_uint4(0, 0, 0, 0);
+    for (int k = 0; k < HBM_V; k++) {
+        const hbm_u4 t = base + k * 256 < n16 ? __builtin_nontemporal_load((const hbm_u4 *)(src + base + k * 256)) : hbm_u4{0, 0, 0, 0};
+        v[k] = make_uint4(t.x, t.y, t.z, t.w);
+    }
     uint32_t acc = 0;
 #pragma unroll
     for (int k = 0; k < HBM_V; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
