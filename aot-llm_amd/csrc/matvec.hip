@@ -29,8 +29,10 @@ constexpr int MAX_SEG = 3;
 // read once per token and streamed past the caches. Measured per kernel in the
 // decode step: 426 -> 461 tok/s on Llama-3-8B, 990 -> 1085 on TinyLlama; the
 // k_mv_kq rows of 10 and 40 super-blocks (Gemma-3's 2560 and 10240 columns)
-// measured slower with it (4096x2560 Q5_K 4.3 -> 5.0 us) and keep plain loads;
-// the Q8_0 kernel measured slower too (Qwen3 decode 234 -> 226 tok/s).
+// measured slower with it (4096x2560 Q5_K 4.3 -> 5.0 us) and keep plain loads.
+// The hint pays only where each load instruction covers whole cache lines
+// (the Q8_0 kernel's two 16-byte halves per block, with it: Qwen3 decode
+// 234 -> 226 tok/s; hence its contiguous runs in k_mv_q8b).
 typedef unsigned nt_u4 __attribute__((ext_vector_type(4)));
 template <bool NT>
 __device__ __forceinline__ uint4 ld_weights(const void *p) {
@@ -1466,6 +1468,8 @@ __global__ __launch_bounds__(256) void k_mv_q80(MvArgs a) {
 constexpr int Q8B_R = 2;  // measured: 2 rows per wave beat 4 (Q8_0 14336x4096 14.5 against 17.7 us) and 1
 constexpr int Q8B_MAX_COLS = 16384;
 constexpr int Q8B_CS = 64 + 4;  // floats per (row, chain) line of the P buffer: chain-major, padded
+// the block of a Q8_0 step that lane l holds after the half swap
+__device__ __forceinline__ int q8_slot(int l) { return (l & 1) * 32 + (l >> 1); }
 
 template <int KIND>
 struct Q8bW {
@@ -1474,7 +1478,7 @@ struct Q8bW {
     uint16_t d;
 };
 
-template <int KIND, bool XQ = false>
+template <int KIND, bool XQ = false, bool RUNS = KIND == AOTK_Q8_0>
 __global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
     constexpr int R = Q8B_R;
     // the activation (cols int8 quants, then cols / 32 scales), sized by the
@@ -1500,18 +1504,35 @@ __global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
         wd[r] = (const uint16_t *)seg_sel(sg, a.w1[0], a.w1[1], a.w1[2]) + (size_t)local * nb;
         wh[r] = KIND == AOTK_Q5_0 ? (const uint32_t *)seg_sel(sg, a.w2[0], a.w2[1], a.w2[2]) + (size_t)local * nb : nullptr;
     }
+    // Q8_0 with RUNS: the step's 64 blocks of 32 bytes are read as two
+    // contiguous 1 KB runs with the nontemporal hint, lane l taking half
+    // l & 1 of block l >> 1 (w0) and of block 32 + (l >> 1) (w1), so that
+    // each load instruction covers whole cache lines (nontemporal loads of
+    // lines split over two instructions fetched them twice); the lane pairs
+    // then swap halves (step), and lane l ends up with block q8_slot(l).
+    // Measured: Qwen3 decode 234 -> 236 tok/s, Q8_0 4096x14336 14.2 -> 13.7
+    // us; the lm-head shape (128256 rows) ran 96 -> 102 us with it and is
+    // launched without (RUNS = false: lane l reads block l with plain loads).
     auto load = [&](Q8bW<KIND> (&w)[R], int c0) {
         const int b = min(c0 + lane, nb - 1);
+        const size_t h0 = (size_t)min(c0 + (lane >> 1), nb - 1) * 32 + (lane & 1) * 16;
+        const size_t h1 = (size_t)min(c0 + 32 + (lane >> 1), nb - 1) * 32 + (lane & 1) * 16;
+        const int bd = min(c0 + q8_slot(lane), nb - 1);
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            if (KIND == AOTK_Q8_0) {
+            if (KIND == AOTK_Q8_0 && RUNS) {
+                w[r].w0 = ld_weights<true>(wq[r] + h0);
+                w[r].w1 = ld_weights<true>(wq[r] + h1);
+                w[r].d = wd[r][bd];
+            } else if (KIND == AOTK_Q8_0) {
                 w[r].w0 = *(const uint4 *)(wq[r] + (size_t)b * 32);
                 w[r].w1 = *(const uint4 *)(wq[r] + (size_t)b * 32 + 16);
+                w[r].d = wd[r][b];
             } else {
-                w[r].w0 = *(const uint4 *)(wq[r] + (size_t)b * 16);
+                w[r].w0 = ld_weights<true>(wq[r] + (size_t)b * 16);
                 if (KIND == AOTK_Q5_0) w[r].qh = wh[r][b];
+                w[r].d = wd[r][b];
             }
-            w[r].d = wd[r][b];
         }
     };
     // the activation's loads first (cols <= 16384: at most 4 quads and one
@@ -1580,9 +1601,26 @@ __global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
     float acc = 0.0f;
     // one step of 64 blocks: phase A (the integer sums and scales into LDS),
     // phase B (the chains)
-    auto step = [&](const Q8bW<KIND> (&w)[R], int c0) {
+    auto step = [&](const Q8bW<KIND> (&w_in)[R], int c0) {
         // phase A
-        const int b = c0 + lane;
+        const int slot = KIND == AOTK_Q8_0 && RUNS ? q8_slot(lane) : lane;
+        const int b = c0 + slot;
+        Q8bW<KIND> w[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            w[r] = w_in[r];
+            if (KIND == AOTK_Q8_0 && RUNS) {
+                // even lanes send their half of block 32 + l/2, odd lanes
+                // theirs of block l/2 (full exec mask: the swap precedes
+                // every branch)
+                const bool odd = lane & 1;
+                const uint4 snd = odd ? w_in[r].w0 : w_in[r].w1;
+                const uint4 rcv = make_uint4(dppx_u<DPP_XOR1>(snd.x), dppx_u<DPP_XOR1>(snd.y),
+                                             dppx_u<DPP_XOR1>(snd.z), dppx_u<DPP_XOR1>(snd.w));
+                w[r].w0 = odd ? rcv : w_in[r].w0;
+                w[r].w1 = odd ? w_in[r].w1 : rcv;
+            }
+        }
         if (b < nb) {
             const uint4 y0 = *(const uint4 *)(sy + b * 32), y1 = *(const uint4 *)(sy + b * 32 + 16);
             const uint32_t yw[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
@@ -1613,8 +1651,8 @@ __global__ __launch_bounds__(256) void k_mv_q8b(MvArgs a) {
                     }
                 }
 #pragma unroll
-                for (int l = 0; l < 8; l++) sP[wave][r][l][lane] = P[l];
-                sD[wave][r][lane] = f16_to_f32(w[r].d) * yd;
+                for (int l = 0; l < 8; l++) sP[wave][r][l][slot] = P[l];
+                sD[wave][r][slot] = f16_to_f32(w[r].d) * yd;
             }
         }
         wave_lds_sync();
@@ -2439,7 +2477,8 @@ static void launch_args(int kind, const MvArgs &a, size_t m, hipStream_t s) {
     case AOTK_Q8_0:
         if (a.cols <= (size_t)Q8B_MAX_COLS) {
             grid.x = (unsigned)((a.total_rows + 4 * Q8B_R - 1) / (4 * Q8B_R));
-            k_mv_q8b<AOTK_Q8_0><<<grid, 256, q8b_lds(a), s>>>(a);
+            if (a.total_rows >= 65536) k_mv_q8b<AOTK_Q8_0, false, false><<<grid, 256, q8b_lds(a), s>>>(a);
+            else k_mv_q8b<AOTK_Q8_0><<<grid, 256, q8b_lds(a), s>>>(a);
         } else {
             grid.x = (unsigned)((a.total_rows + 31) / 32);
             k_mv_q80<AOTK_Q8_0><<<grid, 256, 0, s>>>(a);
