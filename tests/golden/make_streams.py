@@ -78,11 +78,12 @@ def stream(name, threads):
                 final_sha256=digest(lf), final_top_ids=fi, final_top_vals=fv)
 
 
-# Sampled streams (the app.rs:553-610 loop with sampler.rs): configs[0] and
-# configs[2] at their written lengths with --temp 0.8 --top-k 40 --top-p 0.95
+# Sampled streams (the app.rs:553-610 loop with sampler.rs): every config
+# of STREAMS at its written length with --temp 0.8 --top-k 40 --top-p 0.95
 # --repeat-penalty 1.1 (window 64) and seed 42, the penalty window running
 # over the prompt and the generated tokens
-SAMPLED = {"tinyllama-1.1b-q4km": (1, 6, 32), "llama3-8b-q4km": (1, 512, 128)}
+SAMPLED = {"tinyllama-1.1b-q4km": (1, 6, 32), "llama3-8b-q4km": (1, 512, 128),
+           "qwen3-8b-q8_0": (2, 4096, 256), "gemma3-4b-q5km": (2, 8192, 256)}
 SAMPLER = dict(temperature=0.8, top_k=40, top_p=0.95, repeat_penalty=1.1, repeat_last_n=64, seed=42)
 
 
