@@ -111,7 +111,8 @@ def test_oracle_reproduces_tinyllama_stream(oracle):
     m.close()
 
 
-@pytest.mark.parametrize("name,seed,n_prompt,n_gen", [("tinyllama-1.1b-q4km", 1, 6, 32), ("llama3-8b-q4km", 1, 512, 128)])
+@pytest.mark.parametrize("name,seed,n_prompt,n_gen", [("tinyllama-1.1b-q4km", 1, 6, 32), ("llama3-8b-q4km", 1, 512, 128),
+                                                   ("qwen3-8b-q8_0", 2, 4096, 256)])
 def test_sampled_fixture_shape(name, seed, n_prompt, n_gen):
     from aotk import configs
     f = load(f"sampled_{name}.npz")
