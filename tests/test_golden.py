@@ -112,7 +112,8 @@ def test_oracle_reproduces_tinyllama_stream(oracle):
 
 
 @pytest.mark.parametrize("name,seed,n_prompt,n_gen", [("tinyllama-1.1b-q4km", 1, 6, 32), ("llama3-8b-q4km", 1, 512, 128),
-                                                   ("qwen3-8b-q8_0", 2, 4096, 256)])
+                                                   ("qwen3-8b-q8_0", 2, 4096, 256),
+                                                   ("gemma3-4b-q5km", 2, 8192, 256)])
 def test_sampled_fixture_shape(name, seed, n_prompt, n_gen):
     from aotk import configs
     f = load(f"sampled_{name}.npz")

@@ -97,12 +97,13 @@ def test_prefix_continuation_at_config_scale(aotk):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", ["tinyllama-1.1b-q4km", "llama3-8b-q4km", "qwen3-8b-q8_0"])
+@pytest.mark.parametrize("name", ["tinyllama-1.1b-q4km", "llama3-8b-q4km", "qwen3-8b-q8_0", "gemma3-4b-q5km"])
 def test_config_sampled_stream(aotk, name):
     """The sampled loop (app.rs:553-610 with sampler.rs: temperature 0.8,
     top-k 40, top-p 0.95, repeat penalty 1.1 over a 64-token window, seed
     42) on the device at the config's written length (Qwen3: after the
-    4096-token prefill, 256 sampled tokens), against the
+    4096-token prefill, Gemma-3 after the 8192-token one, 256 sampled
+    tokens), against the
     oracle-written fixture (tests/golden/make_streams.py --sampled)."""
     from aotk import configs
     path = os.path.join(GOLDEN, f"sampled_{name}.npz")
