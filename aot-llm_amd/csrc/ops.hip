@@ -996,6 +996,168 @@ __global__ __launch_bounds__(SEQ_T) void k_attn_sv(AttnArgs a) {
     if (tid < DB) a.out[i * (size_t)a.n_head * HD + (size_t)h * HD + d0 + tid] = o;
 }
 
+// Decode attention in one launch for spans of at most AD_MAX_SPAN positions (the
+// scores of k_attn_qk_decode and the softmax and output of k_attn_sv): block
+// = (head, SV_DB dims) as in k_attn_sv. Wave 0 post-processes the head's q,
+// wave 1 the kv head's new k (k_attn_qk_decode's epilogue, the same
+// arithmetic), wave 2 loads the new v row; thread t then forms the score of
+// position t0 + t (the sequential dot product over the head dimension, the
+// new position's k from LDS) straight into registers, and the rest is
+// k_attn_sv's code. Every block of the kv head computes the same new k and
+// v; the first block of the kv head's first query head stores them into the
+// cache, and the products of the new position take v from LDS (its cache
+// row is not written yet when other blocks read). One launch fewer per
+// layer than the scores + softmax/output pair, for the price of each head's
+// scores formed by its HD / SV_DB blocks, each thread reading its position's
+// K row (uncoalesced, from L2). Measured against the pair on Llama-3-8B
+// decode: 486 -> 504 tok/s at ~140 positions, 480 -> 488 at ~270, 474 ->
+// 468 at ~400, 463 -> 430 at ~640; TinyLlama's 38 positions 1080 -> 1159.
+// Hence spans of up to 320 positions.
+constexpr int AD_MAX_SPAN = 320;
+template <int HD>
+__global__ __launch_bounds__(SEQ_T) void k_attn_decode1(AttnArgs a, QkvPost p) {
+    constexpr int DB = SV_DB;
+    constexpr int CP = SV_CP;
+    // scores / exps, padded to a run of 64 (spans below SV_SEQ_MIN: the one-thread sum)
+    static_assert(AD_MAX_SPAN < SV_SEQ_MIN && AD_MAX_SPAN <= SEQ_T, "one position per thread, the one-thread sum");
+    __shared__ __align__(16) float e[AD_MAX_SPAN + 64];
+    __shared__ __align__(16) float prod[2 * SV_BUF + 64];  // product buffers (+64 floats read past the end by the last groups)
+    __shared__ float red[SEQ_T / 64];
+    __shared__ float bc;
+    __shared__ uint64_t stab[32];  // expf's 2^(i/32) table
+    __shared__ __align__(16) float hq[HD], hk[HD], hv[HD];  // post-processed q, new k, new v
+    __shared__ __align__(16) float htmp[2][HD];             // the epilogue's norm scratch
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = tid >> 6;
+    const int h = blockIdx.x / (HD / DB), d0 = (blockIdx.x % (HD / DB)) * DB;
+    const int gqa = a.n_head / a.n_kv_head;
+    const int kvh = h / gqa;
+    size_t t0, n;
+    row_range(a, 0, t0, n);
+    const size_t pos = n - 1;
+    const int cnt = (int)(n - t0);
+    auto at = [&](int t) { return t; };
+    const size_t kv = (size_t)a.n_kv_head * HD;
+    const float *vb = a.v_cache + t0 * kv + (size_t)kvh * HD + d0;
+    const float *cs_row = p.cs + pos * p.rot_dim;
+    // the epilogue's inputs (waves 0 and 1) and the new v row (wave 2)
+    HeadIn<HD> hin;
+    if (wv == 0)
+        head_load<HD>(hin, p.q + (size_t)h * HD, p.bq ? p.bq + (size_t)h * HD : nullptr, p.q_norm, cs_row, (int)p.rot_dim);
+    else if (wv == 1)
+        head_load<HD>(hin, p.k + (size_t)kvh * HD, p.bk ? p.bk + (size_t)kvh * HD : nullptr, p.k_norm, cs_row,
+                      (int)p.rot_dim);
+    else if (wv == 2)
+        for (int e2 = lane; e2 < HD; e2 += 64) {
+            float v = p.v[(size_t)kvh * HD + e2];
+            if (p.bv) v = v + p.bv[(size_t)kvh * HD + e2];
+            hv[e2] = v;
+        }
+    constexpr int R4 = DB / 4;
+    constexpr int NPROD = (SEQ_T / 64 - SEQ_T / 256) * 64;
+    static_assert(CP * R4 == 2 * NPROD, "two float4 per producer thread per chunk");
+    constexpr int PD = 8;
+    float4 ring[PD][2];
+    const int pid = (wv & 3) ? (wv - (wv >> 2) - 1) * 64 + lane : -1;
+    auto issue = [&](float4 (&dst)[2], int c) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int idx = pid + k * NPROD;
+            const int t = c * CP + idx / R4;
+            dst[k] = t < cnt ? *(const float4 *)(vb + (size_t)t * kv + 4 * (idx % R4)) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    constexpr int PE = 2;
+    if (pid >= 0)
+#pragma unroll
+        for (int j = 0; j < PE; j++) issue(ring[j], j);
+    exp_table_to_lds(stab);
+    if (wv == 0) head_post_wave<HD>(hq, htmp[0], hin, p.bq != nullptr, p.q_norm != nullptr, (int)p.rot_dim, p.neox, p.eps);
+    else if (wv == 1) head_post_wave<HD>(hk, htmp[1], hin, p.bk != nullptr, p.k_norm != nullptr, (int)p.rot_dim, p.neox, p.eps);
+    __syncthreads();
+    // the new position's k and v into the cache: one block per kv head
+    if (blockIdx.x == (unsigned)(kvh * gqa * (HD / DB)) && wv == 1) {
+        float *kc = p.k_cache + pos * kv + (size_t)kvh * HD;
+        float *vc = p.v_cache + pos * kv + (size_t)kvh * HD;
+        for (int e2 = lane; e2 < HD; e2 += 64) {
+            kc[e2] = hk[e2];
+            vc[e2] = hv[e2];
+        }
+    }
+    // the scores: thread t, position t0 + t (k_attn_qk_decode's dot product)
+    float sv0 = -INFINITY;
+    if (tid < cnt) {
+        const float4 *kr = t0 + tid == pos ? (const float4 *)hk : (const float4 *)(a.k_cache + (t0 + tid) * kv + (size_t)kvh * HD);
+        const float4 *qq = (const float4 *)hq;
+        float sc = 0.0f;
+#pragma unroll 8
+        for (int d4 = 0; d4 < HD / 4; d4++) {
+            const float4 k4 = kr[d4], q4 = qq[d4];
+            sc += q4.x * k4.x;
+            sc += q4.y * k4.y;
+            sc += q4.z * k4.z;
+            sc += q4.w * k4.w;
+        }
+        sv0 = sc * a.scale;
+    }
+    float mx = wave_max(sv0);
+    if (lane == 0) red[wv] = mx;
+    __syncthreads();
+    mx = wave_max(lane < SEQ_T / 64 ? red[lane] : -INFINITY);
+    if (tid < cnt) e[at(tid)] = aotk_expf_tab(sv0 - mx, stab);
+    if (tid < 64 && cnt + tid < ((cnt + 63) & ~63)) e[cnt + tid] = -0.0f;
+    __syncthreads();
+    if (tid == 0) bc = seq_sum_lds_pad64(e, cnt);
+    __syncthreads();
+    const float sum = bc;
+    const float inv = 1.0f / sum;
+    for (int t = tid; t < cnt; t += SEQ_T) e[at(t)] = e[at(t)] * inv;
+    __syncthreads();  // the sum's scratch is reused for the products below
+    float o = 0.0f;
+    const int nch = (cnt + CP - 1) / CP;
+    if (pid >= 0)
+#pragma unroll
+        for (int j = PE; j < PD; j++) issue(ring[j], j);
+    for (int c0 = 0; c0 < nch; c0 += PD) {
+#pragma unroll
+        for (int j = 0; j < PD; j++) {
+            const int c = c0 + j;
+            if (c < nch) {
+                float *buf = prod + (c & 1) * SV_BUF;
+                const int base = c * CP;
+                const int rows = min(CP, cnt - base);
+                if (pid >= 0) {
+#pragma unroll
+                    for (int k = 0; k < 2; k++) {
+                        const int idx = pid + k * NPROD;
+                        const int r = idx / R4, d = 4 * (idx % R4);
+                        const bool in = r < rows;
+                        const float pt = in ? e[at(base + r)] : 0.0f;
+                        // the new position's v from LDS (its cache row may not be written yet)
+                        const float4 v4 = base + r == cnt - 1 ? *(const float4 *)(hv + d0 + d) : ring[j][k];
+                        buf[(d + 0) * SV_RS + r] = in ? pt * v4.x : -0.0f;
+                        buf[(d + 1) * SV_RS + r] = in ? pt * v4.y : -0.0f;
+                        buf[(d + 2) * SV_RS + r] = in ? pt * v4.z : -0.0f;
+                        buf[(d + 3) * SV_RS + r] = in ? pt * v4.w : -0.0f;
+                    }
+                    issue(ring[j], c + PD);
+                }
+                __syncthreads();
+                if (tid < DB) {
+                    const float *tp = buf + tid * SV_RS;
+                    if (rows > 320) o = lds_chain384(tp, o);
+                    else if (rows > 256) o = lds_chain128(tp + 192, lds_chain192(tp, o));
+                    else if (rows > 192) o = lds_chain256(tp, o);
+                    else if (rows > 128) o = lds_chain192(tp, o);
+                    else if (rows > 64) o = lds_chain128(tp, o);
+                    else o = lds_chain64(tp, o);
+                }
+            }
+        }
+    }
+    if (tid < DB) a.out[(size_t)h * HD + d0 + tid] = o;
+}
+
 // Batched rows (prompt chunks), spans up to ATT_MAX_SPAN: the same softmax
 // and output, with the serial chains spread over lanes instead of blocks.
 //   k_attn_softmax_rows: one wave per (row, head) for spans up to
@@ -1382,6 +1544,15 @@ void launch_attention_decode(float *out, const QkvPost &p, size_t ctx_rows, size
     AttnArgs a = attn_args(out, p.q, p.k_cache, p.v_cache, p.n_head, p.n_kv_head, p.head_dim, ctx_rows, pos0, window,
                            pos_dev, scratch);
     size_t span = window > 0 && window < ctx_rows ? window : ctx_rows;
+    if (span <= (size_t)AD_MAX_SPAN) {  // short spans: scores, softmax and output in one launch
+        const dim3 g1((unsigned)(p.n_head * (p.head_dim / SV_DB)), 1);
+        switch (p.head_dim) {
+        case 64: k_attn_decode1<64><<<g1, SEQ_T, 0, s>>>(a, p); break;
+        case 128: k_attn_decode1<128><<<g1, SEQ_T, 0, s>>>(a, p); break;
+        default: k_attn_decode1<256><<<g1, SEQ_T, 0, s>>>(a, p); break;
+        }
+        return;
+    }
     dim3 grid((unsigned)p.n_kv_head, (unsigned)((span + ATT_CH - 1) / ATT_CH), 1);
     const unsigned threads = (unsigned)(64 * (p.n_head / p.n_kv_head + 1));
     switch (p.head_dim) {

@@ -121,6 +121,35 @@ def test_e2e_models_bitexact(aotk, oracle, name):
         ref.close()
 
 
+@pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen3", "tiny-gemma3"])
+@pytest.mark.parametrize("ctx", [320, 321])
+def test_decode_attention_at_the_one_launch_bound(aotk, oracle, name, ctx):
+    """Decode steps at positions ~310 of a state whose context is 320 (every
+    layer's span fits the one-launch decode attention) and 321 (the global
+    layers take the scores + softmax/output pair): streams and last logits
+    equal the oracle's bit for bit (q/k norms in Qwen3, sliding-window local
+    layers in Gemma-3)."""
+    from aotk import configs
+    spec = configs.build(name)
+    blob = oracle.synth_blob(spec, 0x5EED)
+    n = ctx - 10
+    toks = configs.prompt_tokens(3, n, spec.d["vocab"])
+    print(f"[decode1] {name} ctx {ctx}", flush=True)
+    gm = aotk.Model(spec, blob)
+    st = aotk.State(gm, ctx)
+    ref = oracle.Model(spec, blob, ctx)
+    try:
+        st.prompt(toks, batch=64)
+        ref.prompt(toks, batch=64)
+        assert st.generate(n, 8) == ref.generate(n, 8)
+        a, b = st.logits(), ref.logits()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"rel L2 {rel_l2(a, b):.3g}"
+    finally:
+        ref.close()
+        st.free()
+        gm.free()
+
+
 def test_generate_fills_the_whole_context(aotk, oracle):
     """A generation of ctx + 1 tokens from position 0 (forwards at every
     position of the context) keeps all of its token history: the history
